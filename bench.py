@@ -1,0 +1,298 @@
+"""Benchmark of the LSS bev_pool hot path (forward + backward) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config det]
+
+A step is one vtransform-level forward (geometry + camera features -> BEV:
+quantise, kept mask, compaction, sort, pooled sums, Z-collapse) plus its
+backward (BEV gradient -> feature gradient), at the detection shape of
+configs[0] (B=1, 6 x 118 x 32 x 88 frustum = 1,993,728 points, C=80 fp32,
+360 x 360 x 1 BEV) with inputs resident in HBM.  Prints one JSON line.
+
+`value` is frustum points per second over the K timed steps.  `roofline`
+prices the dominant kernel's algorithmic bytes per launch against 8 TB/s
+using its average duration from HIP events recorded around each launch on
+the launch stream.  `cpu_baseline` times the torch-CPU restatement of the
+reference's CPU fallback (oracle/, the checker) on the same inputs.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = 'bev_pool fwd+bwd frustum points/sec and achieved HBM GB/s at det shape, 1 GPU'
+WORKLOAD = {
+    'det': 'det_fp32_b1: configs[0] shape on GPU -- 6 cams x 118 depth x 32 x 88 frustum '
+           '(1,993,728 points), C=80 fp32, BEV 360x360x1 (+-54 m @ 0.3 m), vtransform level',
+    'seg': 'seg_fp32_b1: configs[1] -- same rig, BEV 256x256x1 (+-51.2 m @ 0.4 m)',
+    'train': 'train_fp32_b4: configs[2] -- det shape, B=4, rig perturbations',
+    'hires': 'hires_fp32_b2: configs[4] -- 64x176 fmap, 720x720 BEV, 10% OOB',
+}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def alg_bytes(n_all, n_kept, n_occ, cells, C, s=4):
+    """Algorithmic HBM bytes of one vtransform-level call (geometry read,
+    kept feature rows read, dense BEV written; BEV gradient rows of occupied
+    cells read, full feature gradient written)."""
+    fwd = 12 * n_all + s * C * n_kept + s * C * cells
+    bwd = s * C * n_occ + s * C * n_all
+    return fwd, bwd
+
+
+def kernel_alg_bytes(name, n_all, n_kept, n_occ, cells, C, s=4):
+    """Algorithmic bytes moved by one launch of the named kernel (its share
+    of the path's compulsory traffic plus the index words it must touch)."""
+    table = {
+        # rows of the kept points (read) + occupied-cell rows (written) + sorted keys
+        'accum_rows': s * C * n_kept + 4 * C * n_occ + 8 * n_kept,
+        # full feature gradient (written) + grad rows of occupied cells + ranks
+        'gather_rows': s * C * n_all + s * C * n_occ + 4 * n_all,
+        # dense BEV (written) + occupied rows (read) + cell ranges
+        'rows_to_bev': s * C * cells + 4 * C * n_occ + 8 * cells,
+        # occupied part of the BEV gradient (read) + rows (written) + cell ranges
+        'bev_to_rows': 2 * s * C * n_occ + 8 * cells,
+        # geometry (read) + ranks (written)
+        'quantize_geom': 12 * n_all + 4 * n_all,
+    }
+    return table.get(name)
+
+
+def make_inputs(pkg, name, device):
+    from bevfusion_triton_amd import synthetic
+
+    spec = synthetic.CASES[name]
+    geom_cpu = synthetic.make_geometry(spec)
+    x = synthetic.make_features(spec, device=device)
+    return spec, geom_cpu, x
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=50)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--config', default='det', choices=sorted(WORKLOAD))
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--profile-steps', type=int, default=10,
+                    help='steps run with per-kernel HIP-event timing')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}): the bev_pool path '
+              'shards by batch with no collective; run one process per GPU.', file=sys.stderr)
+        sys.exit(2)
+
+    pkg = __graft_entry__.load_package()
+    from bevfusion_triton_amd import _lib
+
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    log(f'[bench] building inputs for {args.config}')
+    spec, geom_cpu, x_dev = make_inputs(pkg, args.config, dev)
+    geom = geom_cpu.to(dev)
+    x = x_dev.detach().requires_grad_(True)
+    module = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(dev)
+    C = spec.channels
+    n_all = geom[..., 0].numel()
+
+    # index statistics for the algorithmic bytes (outside the timed region)
+    exp = pkg.LSSIndexExport(geom, module.dx, module.bx, module.nx)
+    n_kept = int(exp.perm.numel())
+    n_occ = int(exp.starts.numel())
+    X, Y, Z = (int(v) for v in module.nx)
+    cells = spec.batch * X * Y * Z
+    del exp
+    fwd_b, bwd_b = alg_bytes(n_all, n_kept, n_occ, cells, C)
+
+    out0 = module.bev_pool(geom, x)
+    g = torch.randn(out0.shape, generator=torch.Generator(device=dev).manual_seed(0), device=dev)
+    del out0
+
+    def step():
+        out = module.bev_pool(geom, x)
+        (gx,) = torch.autograd.grad(out, x, g)
+        return out, gx
+
+    log(f'[bench] warmup {args.warmup}')
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    log(f'[bench] timing {args.steps} steps')
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = wall_s * 1e3 / args.steps
+
+    # forward / backward split (HIP events around each half, median)
+    fwd_ms, bwd_ms = [], []
+    for _ in range(20):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        out = module.bev_pool(geom, x)
+        e[1].record()
+        torch.autograd.grad(out, x, g)
+        e[2].record()
+        torch.cuda.synchronize()
+        fwd_ms.append(e[0].elapsed_time(e[1]))
+        bwd_ms.append(e[1].elapsed_time(e[2]))
+    t_fwd = statistics.median(fwd_ms)
+    t_bwd = statistics.median(bwd_ms)
+
+    # per-kernel durations from HIP events on the launch stream
+    log(f'[bench] per-kernel timing over {args.profile_steps} steps')
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    for _ in range(args.profile_steps):
+        step()
+    torch.cuda.synchronize()
+    _lib.timing_enable(False)
+    ktimes = _lib.timing_read()
+    kernels = {}
+    for name, (ms, n) in ktimes.items():
+        kernels[name] = {'avg_us': round(ms * 1e3 / max(n, 1), 2), 'launches': n}
+    dom = max(kernels, key=lambda k: kernels[k]['avg_us'] * kernels[k]['launches'])
+    dom_us = kernels[dom]['avg_us']
+    dom_bytes = kernel_alg_bytes(dom, n_all, n_kept, n_occ, cells, C)
+    for name, k in kernels.items():
+        b = kernel_alg_bytes(name, n_all, n_kept, n_occ, cells, C)
+        if b is not None and k['avg_us'] > 0:
+            k['alg_GBps'] = round(b / (k['avg_us'] * 1e-6) / 1e9, 1)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9 if dom_bytes else None
+
+    traffic = None
+    tfile = ROOT / 'profiles' / f'traffic_{args.config}.json'
+    if tfile.exists():
+        t = json.loads(tfile.read_text())
+        traffic = t.get('kernels', {}).get(dom)
+
+    result = {
+        'metric': METRIC,
+        'value': round(n_all * args.steps / wall_s, 1),
+        'unit': 'frustum points/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(ms_per_step, 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f32',
+        'data': 'synthetic (6-camera rig restating base.py get_geometry; '
+                'softmax(N(0,1)) x N(0,1) features)',
+        'config': {'workload': WORKLOAD[args.config], 'batch': spec.batch, 'channels': C,
+                   'bev': [X, Y, Z], 'frustum_points': n_all},
+        'fwd_us': round(t_fwd * 1e3, 1),
+        'bwd_us': round(t_bwd * 1e3, 1),
+        'gpu_ms_per_step_events': round(gpu_ms / args.steps, 4),
+        'path_alg_bytes': {'fwd': fwd_b, 'bwd': bwd_b, 'n_kept': n_kept, 'n_occ': n_occ,
+                           'cells': cells},
+        'path_achieved_GBps': round((fwd_b + bwd_b) / ((t_fwd + t_bwd) * 1e-3) / 1e9, 1),
+        'path_frac_of_peak': round((fwd_b + bwd_b) / ((t_fwd + t_bwd) * 1e-3) / 1e9
+                                   / HBM_PEAK_GBS, 4),
+        'roofline': {
+            'kernel': dom,
+            'bound': 'hbm',
+            'achieved': round(achieved, 1) if achieved else None,
+            'peak': HBM_PEAK_GBS,
+            'unit': 'GB/s',
+            'frac': round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            'traffic': traffic,
+            'alg_bytes_per_launch': dom_bytes,
+            'avg_us': dom_us,
+        },
+        'kernels': kernels,
+    }
+
+    if not args.no_cpu_baseline:
+        result['cpu_baseline'] = cpu_baseline(spec, geom_cpu, x.detach().cpu(), g.cpu(), n_all)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
+    """The reference's CPU fallback, restated in torch (oracle/torch_fallback):
+    quantise -> kept mask -> compaction -> index_add_ -> permute -> Z-collapse,
+    backward by autograd; same inputs as the GPU run.  Median of 3 after one
+    warm-up at the box's thread share, plus one single-thread run."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import torch_fallback as ref
+
+    dx, bx, nx = ref.gen_dx_bx(spec.xbound, spec.ybound, spec.zbound)
+
+    def one():
+        xr = x_cpu.clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        out = ref.lss_bev_pool(geom_cpu, xr, dx, bx, nx)
+        t1 = time.perf_counter()
+        torch.autograd.grad(out, xr, g_cpu)
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    log(f'[bench] cpu baseline, {threads} threads')
+    one()
+    runs = [one() for _ in range(3)]
+    fwd = statistics.median(r[0] for r in runs)
+    bwd = statistics.median(r[1] for r in runs)
+    torch.set_num_threads(1)
+    log('[bench] cpu baseline, 1 thread')
+    f1, b1 = one()
+    torch.set_num_threads(prev)
+    model = ''
+    try:
+        for line in Path('/proc/cpuinfo').read_text().splitlines():
+            if line.startswith('model name'):
+                model = line.split(':', 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        'value': round(n_all / (fwd + bwd), 1),
+        'unit': 'frustum points/s',
+        'cores': threads,
+        'kind': 'port',
+        'sample': f'full det workload ({n_all} points, C=80): torch-CPU restatement of the '
+                  f'reference fallback, fwd+bwd, median of 3 after 1 warm-up',
+        'fwd_ms': round(fwd * 1e3, 2),
+        'bwd_ms': round(bwd * 1e3, 2),
+        'single_thread': {'value': round(n_all / (f1 + b1), 1), 'fwd_ms': round(f1 * 1e3, 1),
+                          'bwd_ms': round(b1 * 1e3, 1)},
+        'cpu_model': model,
+    }
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,242 @@
+"""Device pipeline of the pooling path: index stage, forward and backward.
+
+Thin torch-side plumbing over the C ABI (``include/bevpool.h``): it allocates
+outputs and scratch with torch's caching allocator on the tensors' device,
+passes raw pointers plus torch's current HIP stream, and keeps the device
+index (ranks, sorted keys, per-cell ranges) for the backward.  Nothing here
+synchronises the device except :func:`read_meta` (used for error reporting
+and the optional interval export).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+_INT32_MAX = 2**31 - 1
+
+
+def require_gpu(*tensors) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                'bevfusion-triton_amd runs the bev_pool path on a ROCm GPU only '
+                f'(got a tensor on {t.device}); there is no CPU fallback'
+            )
+
+
+class PoolIndex:
+    """Device-resident index of one pooling call.
+
+    rank        int32 (n_points,)  flattened (b, z, x, y) cell, -1 if dropped
+    keys        int64 (n_points,)  first n_kept: sorted (rank << 32 | point)
+    cell_start  int32 (n_cells,)   sorted range [start, end) of each cell
+    cell_end    int32 (n_cells,)
+    meta        int32 (8,)         device counters (n_kept, n_intervals, ...)
+    """
+
+    __slots__ = ('rank', 'keys', 'cell_start', 'cell_end', 'meta', 'n_points', 'B', 'D', 'H',
+                 'W', 'device')
+
+    def __init__(self, n_points, B, D, H, W, device):
+        self.n_points, self.B, self.D, self.H, self.W = int(n_points), int(B), int(D), int(H), int(W)
+        self.device = device
+        n_cells = self.n_cells
+        self.rank = torch.empty(self.n_points, dtype=torch.int32, device=device)
+        self.keys = torch.empty(self.n_points, dtype=torch.int64, device=device)
+        self.cell_start = torch.empty(n_cells, dtype=torch.int32, device=device)
+        self.cell_end = torch.empty(n_cells, dtype=torch.int32, device=device)
+        self.meta = torch.empty(L.META_LEN, dtype=torch.int32, device=device)
+
+    @property
+    def n_cells(self) -> int:
+        return self.B * self.D * self.H * self.W
+
+    def workspace(self):
+        nbytes = L.library().bevpool_index_workspace_bytes(self.n_points, self.n_cells)
+        return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
+
+
+def _check_sizes(n_points: int, n_cells: int) -> None:
+    if n_points > _INT32_MAX:
+        raise ValueError(f'{n_points} points exceed the 2^31-1 limit of the int32 index')
+    if n_cells > _INT32_MAX:
+        raise ValueError(f'B*D*H*W = {n_cells} exceeds the 2^31-1 limit of the int32 ranks')
+
+
+def _sort(idx: PoolIndex, ws, stream) -> None:
+    lib = L.library()
+    L.check(
+        lib.bevpool_sort(
+            L.ptr(idx.rank), idx.n_points, idx.n_cells, L.ptr(idx.keys), L.ptr(idx.cell_start),
+            L.ptr(idx.cell_end), L.ptr(idx.meta), L.ptr(ws), ws.numel(), stream,
+        ),
+        'bevpool_sort',
+    )
+
+
+def index_from_geom(geom2d, B: int, offset, dx, nx) -> PoolIndex:
+    """Quantise (N_all, 3) fp32 geometry in batch-major point order, keep the
+    in-bounds points, stable-sort their ranks and build per-cell ranges.
+
+    offset, dx: 3 fp32 values (offset = fp32(bx) - fp32(dx)/2); nx: 3 ints.
+    Output grid (D, H, W) = (nx[2], nx[0], nx[1]).
+    """
+    require_gpu(geom2d)
+    if geom2d.dtype != torch.float32:
+        raise TypeError('geometry must be float32')
+    if geom2d.dim() != 2 or geom2d.shape[1] != 3:
+        raise ValueError('geometry must be (N, 3)')
+    if geom2d.stride(1) != 1:
+        geom2d = geom2d.contiguous()
+    n_points = geom2d.shape[0]
+    nx = [int(v) for v in nx]
+    B = int(B)
+    _check_sizes(n_points, B * nx[0] * nx[1] * nx[2])
+    if n_points % B:
+        raise ValueError('the point count must be a multiple of the batch size')
+    idx = PoolIndex(n_points, B, nx[2], nx[0], nx[1], geom2d.device)
+    ws = idx.workspace()
+    stream = L.stream_handle(geom2d.device)
+    lib = L.library()
+    off = np.asarray(offset, dtype=np.float32)
+    d = np.asarray(dx, dtype=np.float32)
+    with torch.cuda.device(geom2d.device):
+        _quantize(lib, geom2d, n_points, B, off, d, nx, idx, ws, stream)
+        _sort(idx, ws, stream)
+    return idx
+
+
+def _quantize(lib, geom2d, n_points, B, off, d, nx, idx, ws, stream):
+    L.check(
+        lib.bevpool_quantize_geom(
+            L.ptr(geom2d), n_points, geom2d.stride(0) if n_points else 3,
+            max(1, n_points // B), B,
+            L._f3(*[float(v) for v in off]), L._f3(*[float(v) for v in d]), L._i3(*nx),
+            L.ptr(idx.rank), L.ptr(idx.meta), L.ptr(ws), ws.numel(), stream,
+        ),
+        'bevpool_quantize_geom',
+    )
+
+
+def index_from_coords(coords, B: int, D: int, H: int, W: int) -> PoolIndex:
+    """Op-level ranks from (N, 4) int32/int64 coords (x, y, z, b), then the
+    same sort and per-cell ranges.  Invalid ranks are excluded and counted in
+    meta (see :func:`raise_on_bad_coords`)."""
+    require_gpu(coords)
+    if coords.stride(1) != 1:
+        coords = coords.contiguous()
+    n_points = coords.shape[0]
+    _check_sizes(n_points, B * D * H * W)
+    idx = PoolIndex(n_points, B, D, H, W, coords.device)
+    ws = idx.workspace()
+    stream = L.stream_handle(coords.device)
+    with torch.cuda.device(coords.device):
+        _coord_ranks(coords, n_points, B, D, H, W, idx, ws, stream)
+        _sort(idx, ws, stream)
+    return idx
+
+
+def _coord_ranks(coords, n_points, B, D, H, W, idx, ws, stream):
+    L.check(
+        L.library().bevpool_coord_ranks(
+            L.ptr(coords), coords.element_size(), n_points, coords.stride(0) if n_points else 4,
+            B, D, H, W, L.ptr(idx.rank), L.ptr(idx.meta), L.ptr(ws), ws.numel(), stream,
+        ),
+        'bevpool_coord_ranks',
+    )
+
+
+def read_meta(idx: PoolIndex) -> np.ndarray:
+    """Device counters on the host (synchronises the stream)."""
+    return idx.meta.cpu().numpy()
+
+
+def raise_on_bad_coords(idx: PoolIndex, coords) -> None:
+    """Raise the error the reference CPU fallback's index_add_ raises
+    (``RuntimeError: index ... is out of bounds``) when a coordinate's rank
+    lies outside [0, B*D*H*W).  Synchronises."""
+    meta = read_meta(idx)
+    if meta[L.META_N_BAD]:
+        p = int(meta[L.META_FIRST_BAD])
+        x, y, z, b = (int(v) for v in coords[p].tolist())
+        r = ((b * idx.D + z) * idx.H + x) * idx.W + y
+        raise RuntimeError(
+            f'index {r} is out of bounds for dimension 0 with size {idx.n_cells} '
+            f'(point {p}, coords (x={x}, y={y}, z={z}, b={b}))'
+        )
+
+
+def intervals(idx: PoolIndex):
+    """(starts, lengths, cells) int32 of the occupied cells in rank order
+    (synchronises once to read the interval count)."""
+    n = idx.n_points
+    cap = max(1, n)
+    starts = torch.empty(cap, dtype=torch.int32, device=idx.device)
+    lengths = torch.empty(cap, dtype=torch.int32, device=idx.device)
+    cells = torch.empty(cap, dtype=torch.int32, device=idx.device)
+    ws = idx.workspace()
+    with torch.cuda.device(idx.device):
+        _intervals(idx, n, starts, lengths, cells, ws)
+    m = int(read_meta(idx)[L.META_N_INTERVALS])
+    return starts[:m], lengths[:m], cells[:m]
+
+
+def _intervals(idx, n, starts, lengths, cells, ws):
+    L.check(
+        L.library().bevpool_intervals(
+            L.ptr(idx.keys), n, L.ptr(idx.cell_end), L.ptr(starts), L.ptr(lengths), L.ptr(cells),
+            L.ptr(idx.meta), L.ptr(ws), ws.numel(), L.stream_handle(idx.device),
+        ),
+        'bevpool_intervals',
+    )
+
+
+def forward(idx: PoolIndex, feats2d, out, stride_b: int, stride_c: int, stride_z: int) -> None:
+    """Pool (n_points, C) rows into `out` (element (b, c, z, xy) at
+    b*stride_b + c*stride_c + z*stride_z + xy)."""
+    dtype = L.DTYPE_CODES[feats2d.dtype]
+    C = feats2d.shape[1]
+    if feats2d.stride(1) != 1 and idx.n_points:
+        feats2d = feats2d.contiguous()
+    lib = L.library()
+    scratch_bytes = lib.bevpool_forward_scratch_bytes(idx.n_cells, C)
+    scratch = torch.empty(max(int(scratch_bytes), 256), dtype=torch.uint8, device=idx.device)
+    with torch.cuda.device(idx.device):
+        _forward_call(lib, idx, feats2d, dtype, C, out, stride_b, stride_c, stride_z, scratch)
+
+
+def _forward_call(lib, idx, feats2d, dtype, C, out, stride_b, stride_c, stride_z, scratch):
+    L.check(
+        lib.bevpool_forward(
+            L.ptr(feats2d), dtype, feats2d.stride(0) if idx.n_points else C, C, idx.n_points,
+            L.ptr(idx.keys), L.ptr(idx.cell_start), L.ptr(idx.cell_end), L.ptr(idx.meta), idx.B,
+            idx.D, idx.H * idx.W, stride_b, stride_c, stride_z, L.ptr(out), L.ptr(scratch),
+            scratch.numel(), L.stream_handle(idx.device),
+        ),
+        'bevpool_forward',
+    )
+
+
+def backward(idx: PoolIndex, grad, C: int, stride_b: int, stride_c: int, stride_z: int,
+             x_grad) -> None:
+    """x_grad (n_points, C) <- grad (element (b, c, z, xy) at the strides)."""
+    dtype = L.DTYPE_CODES[grad.dtype]
+    lib = L.library()
+    scratch_bytes = lib.bevpool_backward_scratch_bytes(idx.n_cells, C, dtype)
+    scratch = torch.empty(max(int(scratch_bytes), 256), dtype=torch.uint8, device=idx.device)
+    with torch.cuda.device(idx.device):
+        _backward_call(lib, idx, grad, dtype, C, stride_b, stride_c, stride_z, x_grad, scratch)
+
+
+def _backward_call(lib, idx, grad, dtype, C, stride_b, stride_c, stride_z, x_grad, scratch):
+    L.check(
+        lib.bevpool_backward(
+            L.ptr(grad), dtype, stride_b, stride_c, stride_z, C, L.ptr(idx.rank), idx.n_points,
+            L.ptr(idx.cell_start), L.ptr(idx.cell_end), idx.B, idx.D, idx.H * idx.W,
+            L.ptr(x_grad), x_grad.stride(0) if idx.n_points else C, L.ptr(scratch),
+            scratch.numel(), L.stream_handle(idx.device),
+        ),
+        'bevpool_backward',
+    )

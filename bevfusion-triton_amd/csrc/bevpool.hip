@@ -1,0 +1,1159 @@
+// bevpool.hip -- gfx950 (MI355X, CDNA4) kernels and C ABI for the LSS
+// camera-to-BEV pooling path of ziyangyeh/bevfusion-triton.
+//
+// Pipeline (all stream-ordered on the caller's stream, no host sync):
+//
+//   index stage
+//     quantize_geom_kernel / coord_ranks_kernel  point -> int32 rank (-1 dropped)
+//                                                + radix pass-0 block histogram
+//     radix_scan_kernel                          per-digit exclusive scan of the
+//                                                block histograms (+ zero cell ranges)
+//     radix_scatter_kernel<from_rank>            stable wave-ballot ranked scatter;
+//                                                pass 0 also compacts kept points
+//     radix_hist_kernel                          block histograms of passes >= 1
+//     cell_ranges_kernel                         dense [start, end) per cell
+//     count_starts_kernel + scan_counts_kernel
+//       + interval_write_kernel                  compacted interval starts/lengths
+//   forward
+//     accum_rows_kernel<T>      ranges of sorted points (snapped to cell
+//                               boundaries), rows staged through LDS, one
+//                               sequential fp32 accumulator per channel
+//     rows_to_bev_kernel<T>     cell-major rows -> channel-first tile via LDS
+//                               transpose; empty cells written as zero
+//   backward
+//     bev_to_rows_kernel<T>     channel-first grad tile -> cell-major rows
+//                               (occupied cells only) via LDS transpose
+//     gather_rows_kernel<V>     point-order streaming copy of each point's
+//                               cell row (zero rows for dropped points)
+//
+// Numerics: the quantisation is IEEE fp32 subtraction followed by a correctly
+// rounded fp32 division (built without fast-math, with
+// -fhip-fp32-correctly-rounded-divide-sqrt and -ffp-contract=off), exactly as
+// torch evaluates ((g - (bx - dx/2)) / dx) on the CPU.  Forward sums start at
+// +0.0 and add the cell's points in increasing point index order, which is
+// the order torch's CPU index_add_ uses, so fp32 results are bit-identical.
+
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "bevpool.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// constants
+// ---------------------------------------------------------------------------
+constexpr int kThreads = 256;              // threads per block, every kernel
+constexpr int kWaves = kThreads / 64;      // wave64 waves per block
+constexpr int kItems = 16;                 // keys per thread in sort kernels
+constexpr int kSortTile = kThreads * kItems;  // 4096 keys per sort block
+constexpr int kWaveItems = 64 * kItems;    // 1024 keys per wave in the scatter
+constexpr int kMaxDigitBits = 10;
+constexpr int kMaxRadix = 1 << kMaxDigitBits;
+constexpr int kCellTile = 64;              // cells per transpose tile
+constexpr int64_t kRangePoints = 512;      // nominal sorted points per forward range
+
+// ---------------------------------------------------------------------------
+// error reporting
+// ---------------------------------------------------------------------------
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(BEVPOOL_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return BEVPOOL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// optional per-kernel timing (benchmark instrumentation)
+// ---------------------------------------------------------------------------
+struct TimingRecord {
+  const char *name;
+  hipEvent_t start, stop;
+};
+struct TimingTotal {
+  double ms = 0.0;
+  int64_t launches = 0;
+};
+std::mutex g_timing_mu;
+bool g_timing_enabled = false;
+std::vector<TimingRecord> g_timing_pending;
+std::vector<hipEvent_t> g_event_pool;
+std::vector<std::pair<std::string, TimingTotal>> g_timing_totals;
+
+hipEvent_t take_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Brackets one kernel launch with events when timing is enabled.
+struct LaunchTimer {
+  const char *name;
+  hipStream_t stream;
+  hipEvent_t start = nullptr, stop = nullptr;
+  LaunchTimer(const char *n, hipStream_t s) : name(n), stream(s) {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    if (!g_timing_enabled) return;
+    start = take_event();
+    stop = take_event();
+    if (start && stop) (void)hipEventRecord(start, stream);
+  }
+  ~LaunchTimer() {
+    if (!start || !stop) return;
+    (void)hipEventRecord(stop, stream);
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    g_timing_pending.push_back({name, start, stop});
+  }
+};
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ uint64_t lanes_below() {
+  return (uint64_t(1) << lane_id()) - 1;
+}
+
+__device__ __forceinline__ int key_rank(uint64_t k) { return int(uint32_t(k >> 32)); }
+__device__ __forceinline__ uint32_t key_index(uint64_t k) { return uint32_t(k); }
+
+__device__ __forceinline__ unsigned key_digit(uint64_t k, int shift, unsigned mask) {
+  return unsigned(k >> (32 + shift)) & mask;
+}
+
+// Exclusive scan of one int per thread across a 256-thread block.
+// `scratch` holds kWaves ints.  Every thread must call it.
+__device__ int block_exclusive_scan(int v, int *scratch, int *total) {
+  const int lane = lane_id(), w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) scratch[w] = x;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    int s = scratch[i];
+    before += (i < w) ? s : 0;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + x - v;
+}
+
+// fp32 / fp16 / bf16 element conversion.
+struct F32 {
+  using raw = uint32_t;
+  __device__ static float load(const uint32_t *p) { return __builtin_bit_cast(float, *p); }
+  __device__ static void store(uint32_t *p, float v) { *p = __builtin_bit_cast(uint32_t, v); }
+};
+struct F16 {
+  using raw = uint16_t;
+  __device__ static float load(const uint16_t *p) {
+    return float(__builtin_bit_cast(_Float16, *p));
+  }
+  __device__ static void store(uint16_t *p, float v) {
+    *p = __builtin_bit_cast(uint16_t, _Float16(v));
+  }
+};
+struct BF16 {
+  using raw = uint16_t;
+  __device__ static float load(const uint16_t *p) {
+    return __builtin_bit_cast(float, uint32_t(*p) << 16);
+  }
+  // round to nearest even; NaN -> canonical quiet NaN (torch's c10::BFloat16)
+  __device__ static void store(uint16_t *p, float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+      *p = 0x7fc0;
+      return;
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    *p = uint16_t(u >> 16);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// index stage kernels
+// ---------------------------------------------------------------------------
+
+// models/vtransforms/base.py:139-158: q = ((g - (bx - dx/2)) / dx).long(),
+// kept iff 0 <= q_k < nx[k].  In fp32, trunc(q) in [0, n) <=> q > -1 && q < n
+// (NaN fails both), which avoids converting out-of-range floats.
+// Rank: ops/bev_pool/src/bev_pool_triton.py:34-39 with (D, H, W) = (nz, nx, ny).
+__global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
+    const float *__restrict__ geom, int64_t n_points, int64_t gstride, int64_t ppb, float o0,
+    float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
+    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits) {
+  __shared__ int cnt[kMaxRadix];
+  const int R = 1 << bits;
+  const unsigned mask = unsigned(R - 1);
+  for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
+  __syncthreads();
+  const int64_t base = int64_t(blockIdx.x) * kSortTile;
+  const float f0 = float(n0), f1 = float(n1), f2 = float(n2);
+#pragma unroll 4
+  for (int k = 0; k < kItems; ++k) {
+    const int64_t p = base + int64_t(k) * kThreads + threadIdx.x;
+    if (p < n_points) {
+      const float *g = geom + p * gstride;
+      const float q0 = (g[0] - o0) / d0;
+      const float q1 = (g[1] - o1) / d1;
+      const float q2 = (g[2] - o2) / d2;
+      const bool kept = (q0 > -1.0f) & (q0 < f0) & (q1 > -1.0f) & (q1 < f1) & (q2 > -1.0f) &
+                        (q2 < f2);
+      int r = -1;
+      if (kept) {
+        const int x = int(q0), y = int(q1), z = int(q2);
+        const int b = int(p / ppb);
+        r = ((b * n2 + z) * n0 + x) * n1 + y;
+        atomicAdd(&cnt[unsigned(r) & mask], 1);
+      }
+      rank[p] = r;
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+}
+
+// ops/bev_pool/src/bev_pool_triton.py:34-39 in int64 (wrapping) arithmetic.
+template <typename TC>
+__global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
+    const TC *__restrict__ coords, int64_t n_points, int64_t cstride, int64_t B, int64_t D,
+    int64_t H, int64_t W, int32_t *__restrict__ rank, int32_t *__restrict__ meta,
+    int32_t *__restrict__ hist, int nblocks, int bits) {
+  __shared__ int cnt[kMaxRadix];
+  const int R = 1 << bits;
+  const unsigned mask = unsigned(R - 1);
+  for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
+  __syncthreads();
+  const int64_t base = int64_t(blockIdx.x) * kSortTile;
+  const uint64_t cells = uint64_t(B * D * H * W);
+  for (int k = 0; k < kItems; ++k) {
+    const int64_t p = base + int64_t(k) * kThreads + threadIdx.x;
+    if (p < n_points) {
+      const TC *c = coords + p * cstride;
+      const uint64_t x = uint64_t(int64_t(c[0])), y = uint64_t(int64_t(c[1]));
+      const uint64_t z = uint64_t(int64_t(c[2])), b = uint64_t(int64_t(c[3]));
+      const uint64_t r64 = ((b * uint64_t(D) + z) * uint64_t(H) + x) * uint64_t(W) + y;
+      int r = -1;
+      if (r64 < cells) {  // unsigned compare also rejects negative int64 ranks
+        r = int(r64);
+        atomicAdd(&cnt[unsigned(r) & mask], 1);
+      } else {
+        atomicAdd(&meta[BEVPOOL_META_N_BAD], 1);
+        atomicMin(&meta[BEVPOOL_META_FIRST_BAD], int(p));
+      }
+      rank[p] = r;
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+}
+
+__global__ void init_meta_kernel(int32_t *meta) {
+  if (threadIdx.x < BEVPOOL_META_LEN)
+    meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
+}
+
+// One block per digit: exclusive scan over the blocks of hist[d][*] in place,
+// totals[d] = row sum.  Optionally zeroes the dense cell ranges (grid-stride).
+__global__ __launch_bounds__(kThreads) void radix_scan_kernel(
+    int32_t *__restrict__ hist, int nblocks, int32_t *__restrict__ totals,
+    int32_t *__restrict__ cstart, int32_t *__restrict__ cend, int64_t zero_cells) {
+  __shared__ int scratch[kWaves];
+  int32_t *row = hist + int64_t(blockIdx.x) * nblocks;
+  int carry = 0;
+  for (int t0 = 0; t0 < nblocks; t0 += kThreads * 4) {
+    int v[4], s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = t0 + threadIdx.x * 4 + i;
+      v[i] = j < nblocks ? row[j] : 0;
+      s += v[i];
+    }
+    int tot;
+    int ex = block_exclusive_scan(s, scratch, &tot) + carry;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = t0 + threadIdx.x * 4 + i;
+      if (j < nblocks) row[j] = ex;
+      ex += v[i];
+    }
+    carry += tot;
+  }
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+  for (int64_t c = int64_t(blockIdx.x) * kThreads + threadIdx.x; c < zero_cells;
+       c += int64_t(gridDim.x) * kThreads) {
+    cstart[c] = 0;
+    cend[c] = 0;
+  }
+}
+
+// Block histogram of one digit over the sorted keys of the previous pass.
+__global__ __launch_bounds__(kThreads) void radix_hist_kernel(
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
+    int32_t *__restrict__ hist, int nblocks, int shift, int bits) {
+  __shared__ int cnt[kMaxRadix];
+  const int R = 1 << bits;
+  const unsigned mask = unsigned(R - 1);
+  for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
+  __syncthreads();
+  const int64_t n = meta[BEVPOOL_META_N_KEPT];
+  const int64_t base = int64_t(blockIdx.x) * kSortTile;
+#pragma unroll 4
+  for (int k = 0; k < kItems; ++k) {
+    const int64_t e = base + int64_t(k) * kThreads + threadIdx.x;
+    if (e < n) atomicAdd(&cnt[key_digit(keys[e], shift, mask)], 1);
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+}
+
+// Stable scatter of one LSD radix pass.  Wave w of block b owns the 1024
+// consecutive keys [b*4096 + w*1024, +1024) and walks them 64 at a time in
+// order; a key's destination is
+//   (keys of smaller digits overall) + (same digit in earlier blocks)
+//   + (same digit in earlier waves of this block) + (same digit earlier in
+//   this wave),
+// the last term from a ballot-built peer mask, so equal digits keep their
+// input order.  Pass 0 (kFromRank) reads int32 ranks in point order, skips
+// dropped points (compaction) and builds the (rank << 32 | point) keys.
+template <bool kFromRank>
+__global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
+    const int32_t *__restrict__ rank_in, const uint64_t *__restrict__ keys_in,
+    int64_t n_points, int32_t *__restrict__ meta, uint64_t *__restrict__ keys_out,
+    const int32_t *__restrict__ hist, const int32_t *__restrict__ totals, int nblocks,
+    int shift, int bits) {
+  __shared__ int s_base[kMaxRadix];
+  __shared__ int s_cnt[kWaves * kMaxRadix];
+  __shared__ int s_scan[kWaves];
+  const int R = 1 << bits;
+  const unsigned mask = unsigned(R - 1);
+  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
+  const int64_t n = kFromRank ? n_points : int64_t(meta[BEVPOOL_META_N_KEPT]);
+  const int64_t blk0 = int64_t(blockIdx.x) * kSortTile;
+  if (blk0 >= n) return;  // whole block leaves before any barrier
+
+  // digit bases: exclusive scan of the digit totals + this block's prefix
+  constexpr int kPer = kMaxRadix / kThreads;  // digits per thread (4)
+  int loc[kPer], tsum = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = tid * kPer + i;
+    loc[i] = d < R ? totals[d] : 0;
+    tsum += loc[i];
+  }
+  int total;
+  int ex = block_exclusive_scan(tsum, s_scan, &total);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = tid * kPer + i;
+    if (d < R) s_base[d] = ex + hist[int64_t(d) * nblocks + blockIdx.x];
+    ex += loc[i];
+  }
+  if (kFromRank && blockIdx.x == 0 && tid == 0) meta[BEVPOOL_META_N_KEPT] = total;
+  for (int d = tid; d < kWaves * R; d += kThreads) s_cnt[d] = 0;
+  __syncthreads();
+
+  // this wave's keys, in order; per-wave digit counts
+  uint64_t key[kItems];
+  bool valid[kItems];
+  const int64_t wbase = blk0 + int64_t(w) * kWaveItems;
+  int *cnt = s_cnt + w * R;
+#pragma unroll
+  for (int k = 0; k < kItems; ++k) {
+    const int64_t e = wbase + k * 64 + lane;
+    if (kFromRank) {
+      const int r = e < n ? rank_in[e] : -1;
+      valid[k] = r >= 0;
+      key[k] = (uint64_t(uint32_t(r)) << 32) | uint64_t(uint32_t(e));
+    } else {
+      valid[k] = e < n;
+      key[k] = valid[k] ? keys_in[e] : 0;
+    }
+    if (valid[k]) atomicAdd(&cnt[key_digit(key[k], shift, mask)], 1);
+  }
+  __syncthreads();
+  for (int d = tid; d < R; d += kThreads) {
+    int run = s_base[d];
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const int c = s_cnt[ww * R + d];
+      s_cnt[ww * R + d] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+
+  const uint64_t below_mask = lanes_below();
+#pragma unroll
+  for (int k = 0; k < kItems; ++k) {
+    const unsigned dg = key_digit(key[k], shift, mask);
+    uint64_t peers = __ballot(valid[k]);
+    for (int b = 0; b < bits; ++b) {
+      const bool bit = (dg >> b) & 1u;
+      const uint64_t bal = __ballot(bit);
+      peers &= bit ? bal : ~bal;
+    }
+    if (valid[k]) {
+      const int below = __popcll(peers & below_mask);
+      const int pos = cnt[dg] + below;
+      keys_out[pos] = key[k];
+      if (below == 0) cnt[dg] = pos + __popcll(peers);
+    }
+  }
+}
+
+// bev_pool_legacy.py:56-61 boundary flags on the sorted ranks: writes the
+// dense [start, end) of every occupied cell.
+__global__ __launch_bounds__(kThreads) void cell_ranges_kernel(
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
+    int32_t *__restrict__ cstart, int32_t *__restrict__ cend) {
+  const int64_t n = meta[BEVPOOL_META_N_KEPT];
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int r = key_rank(keys[i]);
+  if (i == 0 || key_rank(keys[i - 1]) != r) cstart[r] = int(i);
+  if (i + 1 == n || key_rank(keys[i + 1]) != r) cend[r] = int(i + 1);
+}
+
+// Interval starts (r[i] != r[i-1]) per block of 256 sorted keys: wave ballot
+// + popcount, summed over the block's waves.
+__global__ __launch_bounds__(kThreads) void count_starts_kernel(
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
+    int32_t *__restrict__ bcount) {
+  __shared__ int s_w[kWaves];
+  const int64_t n = meta[BEVPOOL_META_N_KEPT];
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  bool is_start = false;
+  if (i < n) is_start = (i == 0) || key_rank(keys[i - 1]) != key_rank(keys[i]);
+  const uint64_t b = __ballot(is_start);
+  if (lane_id() == 0) s_w[threadIdx.x >> 6] = __popcll(b);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int s = 0;
+    for (int j = 0; j < kWaves; ++j) s += s_w[j];
+    bcount[blockIdx.x] = s;
+  }
+}
+
+// Single-block exclusive scan of counts[0..n) in place; *total_out = sum.
+__global__ __launch_bounds__(kThreads) void scan_counts_kernel(int32_t *__restrict__ counts,
+                                                               int64_t n,
+                                                               int32_t *__restrict__ total_out) {
+  __shared__ int scratch[kWaves];
+  int carry = 0;
+  for (int64_t t0 = 0; t0 < n; t0 += kThreads * 4) {
+    int v[4], s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t j = t0 + threadIdx.x * 4 + i;
+      v[i] = j < n ? counts[j] : 0;
+      s += v[i];
+    }
+    int tot;
+    int ex = block_exclusive_scan(s, scratch, &tot) + carry;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t j = t0 + threadIdx.x * 4 + i;
+      if (j < n) counts[j] = ex;
+      ex += v[i];
+    }
+    carry += tot;
+  }
+  if (threadIdx.x == 0) *total_out = carry;
+}
+
+// Compacted interval j (the j-th start in sorted order): starts[j], lengths[j]
+// (= end - start, the legacy "difference of starts"), cells[j] = rank.
+__global__ __launch_bounds__(kThreads) void interval_write_kernel(
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
+    const int32_t *__restrict__ cend, const int32_t *__restrict__ boff,
+    int32_t *__restrict__ starts, int32_t *__restrict__ lengths, int32_t *__restrict__ cells) {
+  __shared__ int s_w[kWaves];
+  const int64_t n = meta[BEVPOOL_META_N_KEPT];
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int w = threadIdx.x >> 6;
+  bool is_start = false;
+  int r = 0;
+  if (i < n) {
+    r = key_rank(keys[i]);
+    is_start = (i == 0) || key_rank(keys[i - 1]) != r;
+  }
+  const uint64_t b = __ballot(is_start);
+  if (lane_id() == 0) s_w[w] = __popcll(b);
+  __syncthreads();
+  if (is_start) {
+    int off = boff[blockIdx.x] + __popcll(b & lanes_below());
+    for (int j = 0; j < w; ++j) off += s_w[j];
+    starts[off] = int(i);
+    lengths[off] = cend[r] - int(i);
+    cells[off] = r;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// forward kernels
+// ---------------------------------------------------------------------------
+
+// First sorted position >= i that starts a cell (n if none).
+__device__ __forceinline__ int64_t snap_to_cell(int64_t i, int64_t n,
+                                                const uint64_t *__restrict__ keys,
+                                                const int32_t *__restrict__ cend) {
+  if (i <= 0) return 0;
+  if (i >= n) return n;
+  const int r = key_rank(keys[i]);
+  if (key_rank(keys[i - 1]) != r) return i;
+  return cend[r];
+}
+
+// Block b owns the sorted positions [snap(b*P), snap((b+1)*P)): whole cells
+// only, so every cell's sum is one sequential chain.  Rows (feats[point]) of
+// R sorted points at a time are gathered into LDS by all threads; thread c
+// then adds column c of the R rows in order into its fp32 accumulator and
+// stores it to acc[cell*C + c] when the cell ends.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void accum_rows_kernel(
+    const typename T::raw *__restrict__ x, int64_t ld, int C, int CB, int R,
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
+    const int32_t *__restrict__ cend, float *__restrict__ acc, int64_t P) {
+  extern __shared__ float smem[];
+  float *buf = smem;                         // R * CB floats
+  int *rk = reinterpret_cast<int *>(smem + R * CB);  // R + 1 ints
+  const int tid = threadIdx.x;
+  const int64_t n = meta[BEVPOOL_META_N_KEPT];
+  const int64_t r0 = int64_t(blockIdx.x) * P;
+  if (r0 >= n) return;
+  const int64_t s = snap_to_cell(r0, n, keys, cend);
+  const int64_t e = snap_to_cell(r0 + P < n ? r0 + P : n, n, keys, cend);
+  if (s >= e) return;
+  using raw = typename T::raw;
+  for (int c0 = 0; c0 < C; c0 += CB) {
+    const int cb = C - c0 < CB ? C - c0 : CB;
+    float a = 0.0f;
+    for (int64_t base = s; base < e; base += R) {
+      const int rows = int(e - base < R ? e - base : R);
+      __syncthreads();
+      for (int j = tid; j <= rows; j += kThreads)
+        rk[j] = (base + j < e) ? key_rank(keys[base + j]) : -1;
+      for (int slot = tid; slot < rows * cb; slot += kThreads) {
+        const int j = slot / cb, c = slot - j * cb;
+        const int64_t idx = key_index(keys[base + j]);
+        buf[slot] = T::load(reinterpret_cast<const raw *>(x) + idx * ld + c0 + c);
+      }
+      __syncthreads();
+      if (tid < cb) {
+        for (int j = 0; j < rows; ++j) {
+          a += buf[j * cb + tid];
+          const int r = rk[j];
+          if (rk[j + 1] != r) {
+            acc[int64_t(r) * C + c0 + tid] = a;
+            a = 0.0f;
+          }
+        }
+      }
+    }
+  }
+}
+
+// acc rows (cell-major fp32) -> out (channel-first, dtype T), tile of 64 cells
+// x 64 channels through LDS; empty cells are written as 0.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
+    const float *__restrict__ acc, int C, const int32_t *__restrict__ cstart,
+    const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
+    int64_t sc, int64_t sz, typename T::raw *__restrict__ out) {
+  __shared__ float tile[kCellTile][kCellTile + 1];
+  __shared__ int occ[kCellTile];
+  __shared__ int64_t off[kCellTile];
+  const int tid = threadIdx.x;
+  const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
+  if (tid < kCellTile) {
+    const int64_t cell = cell0 + tid;
+    occ[tid] = (cell < n_cells && cend[cell] > cstart[cell]) ? 1 : 0;
+    if (cell < n_cells) {
+      const int64_t per_b = int64_t(n_z) * n_xy;
+      const int64_t b = cell / per_b, rem = cell - b * per_b;
+      const int64_t z = rem / n_xy, xy = rem - z * n_xy;
+      off[tid] = b * sb + z * sz + xy;
+    } else {
+      off[tid] = -1;
+    }
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < C; c0 += kCellTile) {
+    const int cb = C - c0 < kCellTile ? C - c0 : kCellTile;
+    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
+      const int t = idx >> 6, c = idx & 63;
+      float v = 0.0f;
+      if (c < cb && occ[t]) v = acc[(cell0 + t) * C + c0 + c];
+      tile[t][c] = v;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
+      const int c = idx >> 6, t = idx & 63;
+      if (c < cb && off[t] >= 0) T::store(out + off[t] + int64_t(c0 + c) * sc, tile[t][c]);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward kernels
+// ---------------------------------------------------------------------------
+
+// grad (channel-first, any b/c/z strides, xy contiguous) -> cell-major rows of
+// the occupied cells (raw bits copied).
+template <typename TR>
+__global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
+    const TR *__restrict__ grad, int C, const int32_t *__restrict__ cstart,
+    const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
+    int64_t sc, int64_t sz, TR *__restrict__ rows) {
+  __shared__ TR tile[kCellTile][kCellTile + 1];
+  __shared__ int occ[kCellTile];
+  __shared__ int64_t off[kCellTile];
+  const int tid = threadIdx.x;
+  const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
+  int mine = 0;
+  if (tid < kCellTile) {
+    const int64_t cell = cell0 + tid;
+    mine = (cell < n_cells && cend[cell] > cstart[cell]) ? 1 : 0;
+    occ[tid] = mine;
+    if (mine) {
+      const int64_t per_b = int64_t(n_z) * n_xy;
+      const int64_t b = cell / per_b, rem = cell - b * per_b;
+      const int64_t z = rem / n_xy, xy = rem - z * n_xy;
+      off[tid] = b * sb + z * sz + xy;
+    }
+  }
+  if (!__syncthreads_or(mine)) return;  // no occupied cell: nothing to read
+  for (int c0 = 0; c0 < C; c0 += kCellTile) {
+    const int cb = C - c0 < kCellTile ? C - c0 : kCellTile;
+    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
+      const int c = idx >> 6, t = idx & 63;
+      if (c < cb && occ[t]) tile[t][c] = grad[off[t] + int64_t(c0 + c) * sc];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
+      const int t = idx >> 6, c = idx & 63;
+      if (c < cb && occ[t]) rows[(cell0 + t) * C + c0 + c] = tile[t][c];
+    }
+    __syncthreads();
+  }
+}
+
+// x_grad[p, :] = rows[rank[p], :] (kept) or 0 (dropped); point order, so the
+// writes stream.  V is a 16-byte vector when rows allow it, else one element.
+template <typename V>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(
+    const V *__restrict__ rows, int vpr, const int32_t *__restrict__ rank, int64_t n_points,
+    V *__restrict__ xg, int64_t xg_ld) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t p = i / vpr;
+  if (p >= n_points) return;
+  const int q = int(i - p * vpr);
+  const int r = rank[p];
+  V v;
+  if (r >= 0) {
+    v = rows[int64_t(r) * vpr + q];
+  } else {
+    v = V{};
+  }
+  xg[p * xg_ld + q] = v;
+}
+
+// ---------------------------------------------------------------------------
+// host helpers
+// ---------------------------------------------------------------------------
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct DigitPlan {
+  int passes = 1;
+  int bits[4] = {1, 0, 0, 0};
+  int shift[4] = {0, 0, 0, 0};
+};
+
+DigitPlan plan_digits(int64_t n_cells) {
+  int total_bits = 0;
+  for (uint64_t v = uint64_t(n_cells > 1 ? n_cells - 1 : 0); v; v >>= 1) ++total_bits;
+  if (total_bits < 1) total_bits = 1;
+  DigitPlan p;
+  p.passes = int((total_bits + kMaxDigitBits - 1) / kMaxDigitBits);
+  const int per = (total_bits + p.passes - 1) / p.passes;
+  int shift = 0;
+  for (int i = 0; i < p.passes; ++i) {
+    p.shift[i] = shift;
+    p.bits[i] = total_bits - shift < per ? total_bits - shift : per;
+    shift += p.bits[i];
+  }
+  return p;
+}
+
+struct IndexLayout {
+  size_t keys_tmp, hist, totals, bcount, total;
+  int64_t sort_blocks, cell_blocks;
+};
+
+IndexLayout index_layout(int64_t n_points) {
+  IndexLayout L;
+  L.sort_blocks = ceil_div(n_points, kSortTile);
+  L.cell_blocks = ceil_div(n_points, kThreads);
+  size_t o = 0;
+  L.keys_tmp = o;
+  o = align256(o + size_t(n_points) * sizeof(uint64_t));
+  L.hist = o;
+  o = align256(o + size_t(kMaxRadix) * size_t(L.sort_blocks) * sizeof(int32_t));
+  L.totals = o;
+  o = align256(o + size_t(kMaxRadix) * sizeof(int32_t));
+  L.bcount = o;
+  o = align256(o + size_t(L.cell_blocks) * sizeof(int32_t));
+  L.total = o;
+  return L;
+}
+
+template <typename P>
+P *at(void *base, size_t off) {
+  return reinterpret_cast<P *>(static_cast<char *>(base) + off);
+}
+
+int check_index_args(int64_t n_points, int64_t n_cells, const void *rank, const void *meta,
+                     void *ws, size_t ws_bytes) {
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range [0, 2^31)", (long long)n_points);
+  if (n_cells < 1 || n_cells > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "B*D*H*W=%lld out of range [1, 2^31)", (long long)n_cells);
+  if (!meta || !ws) return fail(BEVPOOL_EINVAL, "null meta or workspace");
+  if (n_points > 0 && !rank) return fail(BEVPOOL_EINVAL, "null rank");
+  const size_t need = index_layout(n_points).total;
+  if (ws_bytes < need)
+    return fail(BEVPOOL_ESPACE, "index workspace %zu bytes < required %zu", ws_bytes, need);
+  return BEVPOOL_OK;
+}
+
+size_t dtype_size(int32_t dtype) { return dtype == BEVPOOL_F32 ? 4 : 2; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int bevpool_abi_version(void) { return BEVPOOL_ABI_VERSION; }
+
+const char *bevpool_last_error(void) { return g_last_error.c_str(); }
+
+size_t bevpool_index_workspace_bytes(int64_t n_points, int64_t n_cells) {
+  (void)n_cells;
+  if (n_points < 0) return 0;
+  return index_layout(n_points).total;
+}
+
+int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_stride,
+                          int64_t points_per_batch, int32_t n_batch, const float offset[3],
+                          const float dx[3], const int32_t nx[3], int32_t *rank, int32_t *meta,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  g_last_error.clear();
+  if (!offset || !dx || !nx) return fail(BEVPOOL_EINVAL, "null offset/dx/nx");
+  if (n_batch < 1 || nx[0] < 1 || nx[1] < 1 || nx[2] < 1)
+    return fail(BEVPOOL_EINVAL, "grid sizes must be positive (B=%d nx=%d,%d,%d)", n_batch, nx[0],
+                nx[1], nx[2]);
+  const int64_t n_cells = int64_t(n_batch) * nx[0] * nx[1] * nx[2];
+  int st = check_index_args(n_points, n_cells, rank, meta, workspace, workspace_bytes);
+  if (st) return st;
+  if (n_points > 0 && (!geom || geom_row_stride < 3 || points_per_batch < 1 ||
+                       ceil_div(n_points, points_per_batch) > n_batch))
+    return fail(BEVPOOL_EINVAL, "bad geometry layout (row stride %lld, points/batch %lld)",
+                (long long)geom_row_stride, (long long)points_per_batch);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  {
+    LaunchTimer t("init_meta", s);
+    hipLaunchKernelGGL(init_meta_kernel, dim3(1), dim3(64), 0, s, meta);
+  }
+  if ((st = check_launch("init_meta"))) return st;
+  if (n_points == 0) return BEVPOOL_OK;
+  const IndexLayout L = index_layout(n_points);
+  const DigitPlan plan = plan_digits(n_cells);
+  {
+    LaunchTimer t("quantize_geom", s);
+    hipLaunchKernelGGL(quantize_geom_kernel, dim3(unsigned(L.sort_blocks)), dim3(kThreads), 0, s,
+                       geom, n_points, geom_row_stride, points_per_batch, offset[0], offset[1],
+                       offset[2], dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,
+                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
+  }
+  return check_launch("quantize_geom");
+}
+
+int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_points,
+                        int64_t coords_row_stride, int32_t B, int32_t D, int32_t H, int32_t W,
+                        int32_t *rank, int32_t *meta, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+  g_last_error.clear();
+  if (B < 1 || D < 1 || H < 1 || W < 1)
+    return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
+  if (coord_bytes != 4 && coord_bytes != 8)
+    return fail(BEVPOOL_EINVAL, "coord_bytes must be 4 or 8, got %d", coord_bytes);
+  const int64_t n_cells = int64_t(B) * D * H * W;
+  int st = check_index_args(n_points, n_cells, rank, meta, workspace, workspace_bytes);
+  if (st) return st;
+  if (n_points > 0 && (!coords || coords_row_stride < 4))
+    return fail(BEVPOOL_EINVAL, "bad coords layout");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  {
+    LaunchTimer t("init_meta", s);
+    hipLaunchKernelGGL(init_meta_kernel, dim3(1), dim3(64), 0, s, meta);
+  }
+  if ((st = check_launch("init_meta"))) return st;
+  if (n_points == 0) return BEVPOOL_OK;
+  const IndexLayout L = index_layout(n_points);
+  const DigitPlan plan = plan_digits(n_cells);
+  LaunchTimer t("coord_ranks", s);
+  if (coord_bytes == 4) {
+    hipLaunchKernelGGL(coord_ranks_kernel<int32_t>, dim3(unsigned(L.sort_blocks)), dim3(kThreads),
+                       0, s, static_cast<const int32_t *>(coords), n_points, coords_row_stride,
+                       int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
+                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
+  } else {
+    hipLaunchKernelGGL(coord_ranks_kernel<int64_t>, dim3(unsigned(L.sort_blocks)), dim3(kThreads),
+                       0, s, static_cast<const int64_t *>(coords), n_points, coords_row_stride,
+                       int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
+                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
+  }
+  return check_launch("coord_ranks");
+}
+
+int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_t *keys,
+                 int32_t *cell_start, int32_t *cell_end, int32_t *meta, void *workspace,
+                 size_t workspace_bytes, void *stream) {
+  g_last_error.clear();
+  int st = check_index_args(n_points, n_cells, rank, meta, workspace, workspace_bytes);
+  if (st) return st;
+  if (!cell_start || !cell_end) return fail(BEVPOOL_EINVAL, "null cell_start/cell_end");
+  if (n_points > 0 && !keys) return fail(BEVPOOL_EINVAL, "null keys");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const IndexLayout L = index_layout(n_points);
+  const DigitPlan plan = plan_digits(n_cells);
+  int32_t *hist = at<int32_t>(workspace, L.hist);
+  int32_t *totals = at<int32_t>(workspace, L.totals);
+  uint64_t *tmp = at<uint64_t>(workspace, L.keys_tmp);
+  if (n_points == 0) {
+    // no points: only the dense cell ranges need clearing
+    LaunchTimer t("radix_scan", s);
+    hipLaunchKernelGGL(radix_scan_kernel, dim3(64), dim3(kThreads), 0, s, hist, 0, totals,
+                       cell_start, cell_end, n_cells);
+    return check_launch("radix_scan");
+  }
+  const int nb = int(L.sort_blocks);
+  const uint64_t *src = nullptr;
+  for (int pass = 0; pass < plan.passes; ++pass) {
+    uint64_t *dst = ((plan.passes - 1 - pass) % 2 == 0) ? keys : tmp;
+    if (pass > 0) {
+      LaunchTimer t("radix_hist", s);
+      hipLaunchKernelGGL(radix_hist_kernel, dim3(nb), dim3(kThreads), 0, s, src, meta, hist, nb,
+                         plan.shift[pass], plan.bits[pass]);
+      if ((st = check_launch("radix_hist"))) return st;
+    }
+    {
+      LaunchTimer t("radix_scan", s);
+      hipLaunchKernelGGL(radix_scan_kernel, dim3(1u << plan.bits[pass]), dim3(kThreads), 0, s,
+                         hist, nb, totals, cell_start, cell_end, pass == 0 ? n_cells : 0);
+      if ((st = check_launch("radix_scan"))) return st;
+    }
+    {
+      LaunchTimer t("radix_scatter", s);
+      if (pass == 0) {
+        hipLaunchKernelGGL(radix_scatter_kernel<true>, dim3(nb), dim3(kThreads), 0, s, rank,
+                           nullptr, n_points, meta, dst, hist, totals, nb, plan.shift[pass],
+                           plan.bits[pass]);
+      } else {
+        hipLaunchKernelGGL(radix_scatter_kernel<false>, dim3(nb), dim3(kThreads), 0, s, nullptr,
+                           src, n_points, meta, dst, hist, totals, nb, plan.shift[pass],
+                           plan.bits[pass]);
+      }
+      if ((st = check_launch("radix_scatter"))) return st;
+    }
+    src = dst;
+  }
+  {
+    LaunchTimer t("cell_ranges", s);
+    hipLaunchKernelGGL(cell_ranges_kernel, dim3(unsigned(L.cell_blocks)), dim3(kThreads), 0, s,
+                       keys, meta, cell_start, cell_end);
+  }
+  return check_launch("cell_ranges");
+}
+
+int bevpool_intervals(const uint64_t *keys, int64_t n_points, const int32_t *cell_end,
+                      int32_t *starts, int32_t *lengths, int32_t *cells, int32_t *meta,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+  g_last_error.clear();
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points out of range");
+  if (!meta) return fail(BEVPOOL_EINVAL, "meta is null");
+  const IndexLayout L = index_layout(n_points);
+  if (workspace_bytes < L.total) return fail(BEVPOOL_ESPACE, "index workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int32_t *bcount = at<int32_t>(workspace, L.bcount);
+  if (n_points == 0) {
+    // meta[N_INTERVALS] was zeroed by the rank stage
+    return BEVPOOL_OK;
+  }
+  if (!keys || !cell_end || !starts || !lengths || !cells)
+    return fail(BEVPOOL_EINVAL, "null interval argument");
+  int st;
+  {
+    LaunchTimer t("count_starts", s);
+    hipLaunchKernelGGL(count_starts_kernel, dim3(unsigned(L.cell_blocks)), dim3(kThreads), 0, s,
+                       keys, meta, bcount);
+    if ((st = check_launch("count_starts"))) return st;
+  }
+  {
+    LaunchTimer t("scan_counts", s);
+    hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(kThreads), 0, s, bcount, L.cell_blocks,
+                       meta + BEVPOOL_META_N_INTERVALS);
+    if ((st = check_launch("scan_counts"))) return st;
+  }
+  LaunchTimer t("interval_write", s);
+  hipLaunchKernelGGL(interval_write_kernel, dim3(unsigned(L.cell_blocks)), dim3(kThreads), 0, s,
+                     keys, meta, cell_end, bcount, starts, lengths, cells);
+  return check_launch("interval_write");
+}
+
+size_t bevpool_forward_scratch_bytes(int64_t n_cells, int32_t C) {
+  if (n_cells < 0 || C < 0) return 0;
+  return size_t(n_cells) * size_t(C) * sizeof(float);
+}
+
+int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                    int64_t n_points, const uint64_t *keys, const int32_t *cell_start,
+                    const int32_t *cell_end, const int32_t *meta, int32_t n_batch, int32_t n_z,
+                    int64_t n_xy, int64_t out_stride_b, int64_t out_stride_c,
+                    int64_t out_stride_z, void *out, void *scratch, size_t scratch_bytes,
+                    void *stream) {
+  g_last_error.clear();
+  if (dtype != BEVPOOL_F32 && dtype != BEVPOOL_F16 && dtype != BEVPOOL_BF16)
+    return fail(BEVPOOL_EINVAL, "unsupported dtype code %d", dtype);
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (n_batch < 1 || n_z < 1 || n_xy < 1) return fail(BEVPOOL_EINVAL, "bad grid");
+  const int64_t n_cells = int64_t(n_batch) * n_z * n_xy;
+  if (n_cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "too many cells");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points out of range");
+  if (!out || !cell_start || !cell_end || !meta) return fail(BEVPOOL_EINVAL, "null argument");
+  if (n_points > 0 && (!feats || !keys || feats_row_stride < C))
+    return fail(BEVPOOL_EINVAL, "bad feats layout");
+  if (scratch_bytes < bevpool_forward_scratch_bytes(n_cells, C) || !scratch)
+    return fail(BEVPOOL_ESPACE, "forward scratch too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float *acc = static_cast<float *>(scratch);
+  int st;
+  if (n_points > 0) {
+    const int CB = C < kThreads ? C : kThreads;
+    int R = 8192 / CB;
+    if (R > 64) R = 64;
+    if (R < 1) R = 1;
+    const size_t smem = size_t(R) * CB * sizeof(float) + size_t(R + 1) * sizeof(int);
+    const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
+    LaunchTimer t("accum_rows", s);
+    switch (dtype) {
+      case BEVPOOL_F32:
+        hipLaunchKernelGGL(accum_rows_kernel<F32>, dim3(grid), dim3(kThreads), smem, s,
+                           static_cast<const uint32_t *>(feats), feats_row_stride, C, CB, R, keys,
+                           meta, cell_end, acc, kRangePoints);
+        break;
+      case BEVPOOL_F16:
+        hipLaunchKernelGGL(accum_rows_kernel<F16>, dim3(grid), dim3(kThreads), smem, s,
+                           static_cast<const uint16_t *>(feats), feats_row_stride, C, CB, R, keys,
+                           meta, cell_end, acc, kRangePoints);
+        break;
+      default:
+        hipLaunchKernelGGL(accum_rows_kernel<BF16>, dim3(grid), dim3(kThreads), smem, s,
+                           static_cast<const uint16_t *>(feats), feats_row_stride, C, CB, R, keys,
+                           meta, cell_end, acc, kRangePoints);
+        break;
+    }
+    if ((st = check_launch("accum_rows"))) return st;
+  }
+  const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
+  LaunchTimer t("rows_to_bev", s);
+  switch (dtype) {
+    case BEVPOOL_F32:
+      hipLaunchKernelGGL(rows_to_bev_kernel<F32>, dim3(tiles), dim3(kThreads), 0, s, acc, C,
+                         cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b, out_stride_c,
+                         out_stride_z, static_cast<uint32_t *>(out));
+      break;
+    case BEVPOOL_F16:
+      hipLaunchKernelGGL(rows_to_bev_kernel<F16>, dim3(tiles), dim3(kThreads), 0, s, acc, C,
+                         cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b, out_stride_c,
+                         out_stride_z, static_cast<uint16_t *>(out));
+      break;
+    default:
+      hipLaunchKernelGGL(rows_to_bev_kernel<BF16>, dim3(tiles), dim3(kThreads), 0, s, acc, C,
+                         cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b, out_stride_c,
+                         out_stride_z, static_cast<uint16_t *>(out));
+      break;
+  }
+  return check_launch("rows_to_bev");
+}
+
+size_t bevpool_backward_scratch_bytes(int64_t n_cells, int32_t C, int32_t dtype) {
+  if (n_cells < 0 || C < 0) return 0;
+  return size_t(n_cells) * size_t(C) * dtype_size(dtype);
+}
+
+int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
+                     int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
+                     const int32_t *rank, int64_t n_points, const int32_t *cell_start,
+                     const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                     void *x_grad, int64_t x_grad_row_stride, void *scratch,
+                     size_t scratch_bytes, void *stream) {
+  g_last_error.clear();
+  if (dtype != BEVPOOL_F32 && dtype != BEVPOOL_F16 && dtype != BEVPOOL_BF16)
+    return fail(BEVPOOL_EINVAL, "unsupported dtype code %d", dtype);
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (n_batch < 1 || n_z < 1 || n_xy < 1) return fail(BEVPOOL_EINVAL, "bad grid");
+  const int64_t n_cells = int64_t(n_batch) * n_z * n_xy;
+  if (n_cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "too many cells");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points out of range");
+  if (n_points == 0) return BEVPOOL_OK;
+  if (!grad || !rank || !cell_start || !cell_end || !x_grad)
+    return fail(BEVPOOL_EINVAL, "null argument");
+  if (x_grad_row_stride < C) return fail(BEVPOOL_EINVAL, "bad x_grad row stride");
+  if (!scratch || scratch_bytes < bevpool_backward_scratch_bytes(n_cells, C, dtype))
+    return fail(BEVPOOL_ESPACE, "backward scratch too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t es = dtype_size(dtype);
+  const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
+  int st;
+  {
+    LaunchTimer t("bev_to_rows", s);
+    if (es == 4) {
+      hipLaunchKernelGGL(bev_to_rows_kernel<uint32_t>, dim3(tiles), dim3(kThreads), 0, s,
+                         static_cast<const uint32_t *>(grad), C, cell_start, cell_end, n_cells,
+                         n_z, n_xy, grad_stride_b, grad_stride_c, grad_stride_z,
+                         static_cast<uint32_t *>(scratch));
+    } else {
+      hipLaunchKernelGGL(bev_to_rows_kernel<uint16_t>, dim3(tiles), dim3(kThreads), 0, s,
+                         static_cast<const uint16_t *>(grad), C, cell_start, cell_end, n_cells,
+                         n_z, n_xy, grad_stride_b, grad_stride_c, grad_stride_z,
+                         static_cast<uint16_t *>(scratch));
+    }
+    if ((st = check_launch("bev_to_rows"))) return st;
+  }
+  const size_t row_bytes = size_t(C) * es;
+  const bool vec16 = (row_bytes % 16 == 0) && ((size_t(x_grad_row_stride) * es) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(x_grad) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(scratch) % 16 == 0);
+  LaunchTimer t("gather_rows", s);
+  if (vec16) {
+    const int vpr = int(row_bytes / 16);
+    const int64_t ld = int64_t(size_t(x_grad_row_stride) * es / 16);
+    const unsigned grid = unsigned(ceil_div(n_points * vpr, kThreads));
+    hipLaunchKernelGGL(gather_rows_kernel<uint4>, dim3(grid), dim3(kThreads), 0, s,
+                       static_cast<const uint4 *>(scratch), vpr, rank, n_points,
+                       static_cast<uint4 *>(x_grad), ld);
+  } else if (es == 4) {
+    const unsigned grid = unsigned(ceil_div(n_points * C, kThreads));
+    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3(grid), dim3(kThreads), 0, s,
+                       static_cast<const uint32_t *>(scratch), int(C), rank, n_points,
+                       static_cast<uint32_t *>(x_grad), x_grad_row_stride);
+  } else {
+    const unsigned grid = unsigned(ceil_div(n_points * C, kThreads));
+    hipLaunchKernelGGL(gather_rows_kernel<uint16_t>, dim3(grid), dim3(kThreads), 0, s,
+                       static_cast<const uint16_t *>(scratch), int(C), rank, n_points,
+                       static_cast<uint16_t *>(x_grad), x_grad_row_stride);
+  }
+  return check_launch("gather_rows");
+}
+
+int bevpool_timing_enable(int enable) {
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  g_timing_enabled = enable != 0;
+  return BEVPOOL_OK;
+}
+
+int bevpool_timing_reset(void) {
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  for (auto &r : g_timing_pending) {
+    (void)hipEventSynchronize(r.stop);
+    g_event_pool.push_back(r.start);
+    g_event_pool.push_back(r.stop);
+  }
+  g_timing_pending.clear();
+  g_timing_totals.clear();
+  return BEVPOOL_OK;
+}
+
+int bevpool_timing_read(char *names, int name_stride, double *total_ms, int64_t *launches,
+                        int max_entries) {
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  for (auto &r : g_timing_pending) {
+    if (hipEventSynchronize(r.stop) != hipSuccess)
+      return fail(BEVPOOL_EHIP, "hipEventSynchronize failed");
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess)
+      return fail(BEVPOOL_EHIP, "hipEventElapsedTime failed");
+    bool found = false;
+    for (auto &kv : g_timing_totals) {
+      if (kv.first == r.name) {
+        kv.second.ms += ms;
+        kv.second.launches += 1;
+        found = true;
+        break;
+      }
+    }
+    if (!found) {
+      TimingTotal tt;
+      tt.ms = ms;
+      tt.launches = 1;
+      g_timing_totals.emplace_back(r.name, tt);
+    }
+    g_event_pool.push_back(r.start);
+    g_event_pool.push_back(r.stop);
+  }
+  g_timing_pending.clear();
+  int n = 0;
+  for (auto &kv : g_timing_totals) {
+    if (n >= max_entries) break;
+    if (names && name_stride > 0) {
+      snprintf(names + size_t(n) * name_stride, size_t(name_stride), "%s", kv.first.c_str());
+    }
+    if (total_ms) total_ms[n] = kv.second.ms;
+    if (launches) launches[n] = kv.second.launches;
+    ++n;
+  }
+  return n;
+}
+
+}  // extern "C"

@@ -1,0 +1,153 @@
+"""LSS view-transform pooling (geometry + camera features -> BEV) on MI355X.
+
+Drop-in for the pooling half of ``models/vtransforms/base.py``:
+  * :func:`gen_dx_bx`            -- ``base.py:19-23``
+  * :class:`BevPoolTransform`    -- the ``dx``/``bx``/``nx`` parameters of
+    ``BaseTransform.__init__`` (``base.py:57-60``) and its ``bev_pool(geom_feats, x)``
+    method (``base.py:131-165``): quantise, batch index, kept mask,
+    compaction, ``bev_pool``, Z-collapse;
+  * :func:`lss_bev_pool`         -- the same as a function.
+
+Everything between the geometry/feature tensors and the BEV map runs as HIP
+kernels: the quantisation/kept-mask, the compaction (fused into the first
+radix pass), the sort, the per-cell ranges, the pooled sums and the
+Z-collapse (the output is written directly as (B, C*Dz, H, W)).  The gradient
+flows to ``x`` only (the reference's ``.long()`` cuts it from the geometry),
+with zero rows for dropped points, as autograd of ``x[kept]`` gives.
+
+Like ``@force_fp32`` (``models/helper/amp.py:35-67``) the inputs are cast to
+fp32 first.  ``x`` may be any (B, N, D, fH, fW, C) view whose flattening to
+(N_all, C) has unit channel stride -- a channel-last producer costs no copy;
+otherwise it is copied once, as ``rearrange`` does at ``base.py:136``.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+from torch import nn
+
+from . import _pipeline as P
+
+
+def gen_dx_bx(xbound, ybound, zbound):
+    """``base.py:19-23``: dx = step, bx = lo + step/2 (double -> fp32),
+    nx = int64((hi - lo) / step) with the division in double."""
+    dx = torch.Tensor([row[2] for row in [xbound, ybound, zbound]])
+    bx = torch.Tensor([row[0] + row[2] / 2.0 for row in [xbound, ybound, zbound]])
+    nx = torch.LongTensor([(row[1] - row[0]) / row[2] for row in [xbound, ybound, zbound]])
+    return dx, bx, nx
+
+
+def host_grid(dx, bx, nx):
+    """(offset, dx, nx) on the host: offset = bx - dx/2 evaluated with torch
+    fp32 tensor arithmetic, exactly as ``base.py:139`` evaluates it.  Copies
+    device tensors to the host (a synchronisation)."""
+    dx32 = torch.as_tensor(dx).detach().to('cpu', torch.float32)
+    bx32 = torch.as_tensor(bx).detach().to('cpu', torch.float32)
+    offset = (bx32 - dx32 / 2.0).numpy().astype(np.float32)
+    nxl = [int(v) for v in torch.as_tensor(nx).detach().cpu().tolist()]
+    return offset, dx32.numpy().astype(np.float32), nxl
+
+
+class _LSSBevPool(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, geom_feats, offset, dx, nx):
+        B, N, D, fH, fW, C = x.shape
+        X, Y, Z = nx
+        x2 = x.reshape(B * N * D * fH * fW, C)
+        if x2.stride(1) != 1 and x2.shape[0]:
+            x2 = x2.contiguous()
+        idx = P.index_from_geom(geom_feats.reshape(-1, 3), B, offset, dx, nx)
+        out = torch.empty((B, Z * C, X, Y), dtype=torch.float32, device=x.device)
+        # element (b, c, z, xy) of the (B, C, Dz, H, W) pool at channel z*C + c
+        P.forward(idx, x2, out, Z * C * X * Y, X * Y, C * X * Y)
+        ctx.pool_index = idx
+        ctx.x_shape = x.shape
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        idx = ctx.pool_index
+        C = ctx.x_shape[-1]
+        if g.dtype != torch.float32:
+            g = g.float()
+        if g.stride(3) != 1 or g.stride(2) != idx.W:
+            g = g.contiguous()
+        x_grad = torch.empty(ctx.x_shape, dtype=torch.float32, device=g.device)
+        P.backward(idx, g, C, g.stride(0), g.stride(1), C * g.stride(1),
+                   x_grad.view(-1, C))
+        return x_grad, None, None, None, None
+
+
+def lss_bev_pool(geom_feats, x, dx, bx, nx, *, grid=None):
+    """``BaseTransform.bev_pool`` (``base.py:131-165``) as a function.
+
+    geom_feats (B, N, D, fH, fW, 3), x (B, N, D, fH, fW, C) -> (B, C*Dz, H, W)
+    fp32.  ``grid`` may pass a precomputed :func:`host_grid` triple to avoid
+    reading device-resident dx/bx/nx back to the host on every call.
+    """
+    P.require_gpu(geom_feats, x)
+    if torch.is_floating_point(x):
+        x = x.float()
+    geom_feats = geom_feats.float()
+    if x.dim() != 6 or geom_feats.dim() != 6 or geom_feats.shape[-1] != 3:
+        raise ValueError('expected geom_feats (B, N, D, H, W, 3) and x (B, N, D, H, W, C)')
+    if geom_feats.shape[:5] != x.shape[:5]:
+        raise ValueError('geom_feats and x must agree on (B, N, D, H, W)')
+    offset, d, n = grid if grid is not None else host_grid(dx, bx, nx)
+    return _LSSBevPool.apply(x, geom_feats, offset, d, tuple(n))
+
+
+class BevPoolTransform(nn.Module):
+    """The pooling state and method of ``BaseTransform`` (``base.py:26-66,
+    131-165``): ``dx``, ``bx``, ``nx`` parameters from the x/y/z bounds and
+    ``bev_pool(geom_feats, x)``.  A host copy of the grid is cached (and
+    refreshed if the parameters are modified in place) so the forward never
+    synchronises."""
+
+    def __init__(self, xbound, ybound, zbound):
+        super().__init__()
+        self.xbound, self.ybound, self.zbound = xbound, ybound, zbound
+        dx, bx, nx = gen_dx_bx(xbound, ybound, zbound)
+        self.dx = nn.Parameter(dx, requires_grad=False)
+        self.bx = nn.Parameter(bx, requires_grad=False)
+        self.nx = nn.Parameter(nx, requires_grad=False)
+        self._grid = host_grid(dx, bx, nx)
+        self._grid_key = self._key()
+
+    def _key(self):
+        return tuple((p.data_ptr(), p._version) for p in (self.dx, self.bx, self.nx))
+
+    def grid(self):
+        key = self._key()
+        if key != self._grid_key:
+            self._grid = host_grid(self.dx, self.bx, self.nx)
+            self._grid_key = key
+        return self._grid
+
+    def bev_pool(self, geom_feats, x):
+        return lss_bev_pool(geom_feats, x, self.dx, self.bx, self.nx, grid=self.grid())
+
+    def forward(self, geom_feats, x):
+        return self.bev_pool(geom_feats, x)
+
+
+class LSSIndexExport:
+    """Every index-stage quantity of a vtransform-level call, in original
+    point indices, for parity checks: rank (-1 dropped), kept mask, the stable
+    sort permutation of the kept points, their sorted ranks and the interval
+    starts/lengths.  Synchronises."""
+
+    def __init__(self, geom_feats, dx, bx, nx):
+        P.require_gpu(geom_feats)
+        offset, d, n = host_grid(dx, bx, nx)
+        B = geom_feats.shape[0]
+        idx = P.index_from_geom(geom_feats.float().reshape(-1, 3), B, offset, d, n)
+        n_kept = int(P.read_meta(idx)[0])
+        self.rank = idx.rank.long()
+        self.kept = idx.rank >= 0
+        keys = idx.keys[:n_kept]
+        self.perm = (keys & 0xFFFFFFFF).long()
+        self.sorted_ranks = (keys >> 32).long()
+        self.starts, self.lengths, self.cells = P.intervals(idx)
+        self.index = idx

@@ -1,0 +1,217 @@
+/*
+ * bevpool.h -- C ABI of the MI355X (gfx950) LSS camera-to-BEV pooling library
+ * (libbevpool_amd.so).
+ *
+ * This is the drop-in native boundary for the LSS `bev_pool` hot path of
+ * ziyangyeh/bevfusion-triton.  Every entry point is plain C: raw device
+ * pointers, sizes and a `hipStream_t` passed as `void *`.  No torch types
+ * cross this boundary.
+ *
+ * Conventions shared by every call:
+ *   - all work is stream-ordered on the caller's stream; nothing synchronises
+ *     the device and nothing allocates device memory (the caller passes every
+ *     buffer, including the scratch workspace);
+ *   - the return value is a status code (BEVPOOL_OK == 0, negative on error)
+ *     and bevpool_last_error() returns a thread-local message for the last
+ *     failing call on the calling thread;
+ *   - device-side counters live in a caller-owned `meta` array of
+ *     BEVPOOL_META_LEN int32 (see BEVPOOL_META_*);
+ *   - ranks are the reference's flattened (b, z, x, y) cell index
+ *     ((b*D + z)*H + x)*W + y, stored as int32 (-1 marks a dropped point);
+ *     the library rejects grids with B*D*H*W >= 2^31;
+ *   - sorted keys are uint64 (rank << 32) | point_index, i.e. the stable
+ *     argsort of the ranks expressed as a sort of unique 64-bit keys.
+ *
+ * The reference interfaces each call replaces are cited per declaration
+ * (paths relative to the reference repository root).
+ */
+#ifndef BEVPOOL_AMD_H_
+#define BEVPOOL_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BEVPOOL_ABI_VERSION 1
+
+/* status codes */
+#define BEVPOOL_OK 0
+#define BEVPOOL_EINVAL -1  /* bad argument (shape, size, dtype, alignment)   */
+#define BEVPOOL_EHIP -2    /* a HIP runtime call or kernel launch failed       */
+#define BEVPOOL_ESPACE -3  /* workspace / scratch buffer too small            */
+
+/* element types of feature / gradient tensors */
+#define BEVPOOL_F32 0
+#define BEVPOOL_F16 1
+#define BEVPOOL_BF16 2
+
+/* layout of the caller-owned int32 meta array (device memory) */
+#define BEVPOOL_META_N_KEPT 0      /* number of kept points (sorted keys)     */
+#define BEVPOOL_META_N_INTERVALS 1 /* number of occupied cells (intervals)    */
+#define BEVPOOL_META_N_BAD 2       /* op-level: coords whose rank is invalid  */
+#define BEVPOOL_META_FIRST_BAD 3   /* op-level: smallest invalid point index  */
+#define BEVPOOL_META_LEN 8
+
+/* ABI version of the loaded library (BEVPOOL_ABI_VERSION). */
+int bevpool_abi_version(void);
+
+/* Message describing the last failing call on this thread ("" if none). */
+const char *bevpool_last_error(void);
+
+/*
+ * Bytes of scratch workspace the index stage (quantise/ranks + sort +
+ * intervals) needs for n_points points and n_cells = B*D*H*W cells.
+ * One workspace serves one index stage at a time on one stream.
+ */
+size_t bevpool_index_workspace_bytes(int64_t n_points, int64_t n_cells);
+
+/*
+ * Voxel quantisation + kept mask of LSS geometry, fused with the first pass
+ * of the rank sort (its digit histogram).
+ *
+ * Replaces models/vtransforms/base.py:139-158 (quantise
+ * ((g - (bx - dx/2)) / dx).long(), batch-index concat, in-bounds kept mask)
+ * together with the rank formula of ops/bev_pool/src/bev_pool_triton.py:34-39.
+ *
+ *   geom        fp32 [n_points, 3] (x, y, z) in batch-major point order,
+ *               row stride geom_row_stride floats, component stride 1
+ *   points_per_batch  N*D*fH*fW (point p belongs to batch p / points_per_batch)
+ *   offset[3]   fp32(bx) - fp32(dx)/2, computed in fp32 by the caller
+ *   dx[3]       fp32 voxel size
+ *   nx[3]       grid size (X -> H, Y -> W, Z -> D of the output)
+ *   rank        out: int32 [n_points], -1 for dropped points
+ *   meta        int32 [BEVPOOL_META_LEN], zeroed by this call
+ * Must be followed by bevpool_sort on the same workspace and stream.
+ */
+int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_stride,
+                          int64_t points_per_batch, int32_t n_batch, const float offset[3],
+                          const float dx[3], const int32_t nx[3], int32_t *rank, int32_t *meta,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Op-level ranks from integer coords (columns x, y, z, b), fused with the
+ * first sort pass histogram.
+ *
+ * Replaces ops/bev_pool/src/bev_pool_triton.py:34-39 (_flatten_ranks,
+ * rank = ((b*D + z)*H + x)*W + y in int64 arithmetic).  A rank outside
+ * [0, B*D*H*W) is what makes the reference CPU fallback's index_add_
+ * (bev_pool_triton.py:47) raise; here such a point is excluded (rank -1),
+ * counted in meta[BEVPOOL_META_N_BAD] and its index min-reduced into
+ * meta[BEVPOOL_META_FIRST_BAD] so the host can raise the same error.
+ *
+ *   coords       int32 or int64 (coord_bytes 4 or 8) [n_points, 4],
+ *                row stride coords_row_stride elements, column stride 1
+ */
+int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_points,
+                        int64_t coords_row_stride, int32_t B, int32_t D, int32_t H, int32_t W,
+                        int32_t *rank, int32_t *meta, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+/*
+ * Stream compaction of kept points + stable LSD radix sort of their ranks
+ * + dense per-cell point ranges.
+ *
+ * Replaces the kept-point compaction of models/vtransforms/base.py:157-158
+ * and the sort of ops/bev_pool/bev_pool_legacy.py:102-104, with the legacy
+ * (x,y,z,b) ranks replaced by the (b,z,x,y) ranks above and the sort made
+ * stable, so the permutation equals a stable argsort of the ranks.
+ *
+ *   rank         int32 [n_points] from bevpool_quantize_geom / bevpool_coord_ranks
+ *   keys         out: uint64 [n_points]; the first meta[N_KEPT] entries are
+ *                the sorted (rank << 32 | point_index) keys
+ *   cell_start,
+ *   cell_end     out: int32 [n_cells]; the sorted positions [start, end) of
+ *                each cell's points (start == end == 0 for an empty cell)
+ *   meta         meta[BEVPOOL_META_N_KEPT] is written
+ */
+int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_t *keys,
+                 int32_t *cell_start, int32_t *cell_end, int32_t *meta, void *workspace,
+                 size_t workspace_bytes, void *stream);
+
+/*
+ * Interval boundaries of the sorted ranks, compacted in rank order.
+ *
+ * Replaces ops/bev_pool/bev_pool_legacy.py:56-61 (boundary flags
+ * r[i] != r[i-1], interval_starts = where(flags), lengths by difference with
+ * the last one n - start) without the host synchronisation of torch.where.
+ *
+ *   starts, lengths, cells   out: int32 [n_points] (capacity); the first
+ *                meta[BEVPOOL_META_N_INTERVALS] entries are written
+ */
+int bevpool_intervals(const uint64_t *keys, int64_t n_points, const int32_t *cell_end,
+                      int32_t *starts, int32_t *lengths, int32_t *cells, int32_t *meta,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* Bytes of fp32 scratch bevpool_forward needs: n_cells * C * 4. */
+size_t bevpool_forward_scratch_bytes(int64_t n_cells, int32_t C);
+
+/*
+ * Forward pooling: out[cell, c] = sum over the cell's points, in increasing
+ * point order, of feats[p, c], accumulated in fp32 from +0.0, written
+ * channel-first with empty cells set to zero.
+ *
+ * Replaces ops/bev_pool/src/bev_pool_triton.py:42-48 (index_add_ fallback),
+ * :155-186 (forward of the autograd Function), the permute of :227, and the
+ * Z-collapse of models/vtransforms/base.py:163 (through the output strides);
+ * legacy equivalent ops/bev_pool/csrc/bev_pool_cuda.cu:20-42.
+ *
+ *   feats        dtype [n_points, C], row stride feats_row_stride elements,
+ *                channel stride 1 (rows are indexed by the keys' point index)
+ *   out          dtype; element (b, c, z, xy) at
+ *                b*out_stride_b + c*out_stride_c + z*out_stride_z + xy
+ *                with xy = x*W + y in [0, n_xy)
+ *   scratch      >= bevpool_forward_scratch_bytes(n_cells, C) bytes
+ */
+int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                    int64_t n_points, const uint64_t *keys, const int32_t *cell_start,
+                    const int32_t *cell_end, const int32_t *meta, int32_t n_batch, int32_t n_z,
+                    int64_t n_xy, int64_t out_stride_b, int64_t out_stride_c,
+                    int64_t out_stride_z, void *out, void *scratch, size_t scratch_bytes,
+                    void *stream);
+
+/* Bytes of scratch bevpool_backward needs: n_cells * C * element size. */
+size_t bevpool_backward_scratch_bytes(int64_t n_cells, int32_t C, int32_t dtype);
+
+/*
+ * Backward pooling: x_grad[p, :] = grad[b, :, z, xy] of p's cell for a kept
+ * point and 0 for a dropped one (rank -1).  A pure copy of the gradient's
+ * bits.
+ *
+ * Replaces ops/bev_pool/src/bev_pool_triton.py:102-150 and :189-216 (the
+ * gather backward, including the out_grad.contiguous() transpose of :192)
+ * and the zero-filled gradient of the kept-mask gather of
+ * models/vtransforms/base.py:157; legacy equivalent
+ * ops/bev_pool/csrc/bev_pool_cuda.cu:61-84.
+ *
+ *   grad         dtype; element (b, c, z, xy) at
+ *                b*grad_stride_b + c*grad_stride_c + z*grad_stride_z + xy
+ *   x_grad       out: dtype [n_points, C], row stride x_grad_row_stride
+ *   scratch      >= bevpool_backward_scratch_bytes(n_cells, C, dtype) bytes
+ */
+int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
+                     int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
+                     const int32_t *rank, int64_t n_points, const int32_t *cell_start,
+                     const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                     void *x_grad, int64_t x_grad_row_stride, void *scratch,
+                     size_t scratch_bytes, void *stream);
+
+/*
+ * Optional per-kernel timing.  When enabled, every kernel launch is bracketed
+ * by HIP events on the launch stream; bevpool_timing_read() synchronises
+ * those events and returns, per kernel name, the summed milliseconds and
+ * launch count since the last reset.  Used by the benchmark only.
+ */
+int bevpool_timing_enable(int enable);
+int bevpool_timing_reset(void);
+/* Writes up to max_entries entries; returns the number of entries or < 0. */
+int bevpool_timing_read(char *names, int name_stride, double *total_ms, int64_t *launches,
+                        int max_entries);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BEVPOOL_AMD_H_ */

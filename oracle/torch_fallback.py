@@ -1,0 +1,188 @@
+"""torch-CPU restatement of the reference's CPU fallback for the bev_pool path.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): the checker for the
+HIP path and the CPU baseline of ``bench.py``.  Every function restates the
+reference file:line it cites; none of it is imported by the library.
+
+Pinning (see ``tests/test_oracle.py``):
+  gen_dx_bx        closed form (double arithmetic -> fp32 / int64 truncation),
+                   values for the det/seg/hires grids.
+  quantize         hand-derived edge vectors (truncation of q in (-1, 0),
+                   NaN/inf, the exact upper bound) + the C restatement.
+  flatten_ranks    closed form on tiny inputs + the C restatement.
+  bev_pool_cpu     the reference's known-answer fixture (exact), brute-force
+                   Python loops, numpy.add.at, and the C sequential sum.
+  sort_perm        brute-force sorted((rank, index)) on tiny inputs.
+  intervals        brute-force run-length encoding on tiny inputs.
+  backward         brute-force gather on tiny inputs + the C restatement.
+"""
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+
+# ---------------------------------------------------------------------------
+# models/vtransforms/base.py:19-23
+# ---------------------------------------------------------------------------
+def gen_dx_bx(xbound, ybound, zbound):
+    """dx = step, bx = lo + step/2 (Python double -> fp32), nx = (hi-lo)/step
+    (double division, then int64 truncation) -- ``base.py:19-23``."""
+    rows = [xbound, ybound, zbound]
+    dx = torch.tensor([row[2] for row in rows], dtype=torch.float32)
+    bx = torch.tensor([row[0] + row[2] / 2.0 for row in rows], dtype=torch.float32)
+    nx = torch.tensor([int((row[1] - row[0]) / row[2]) for row in rows], dtype=torch.int64)
+    return dx, bx, nx
+
+
+# ---------------------------------------------------------------------------
+# ops/bev_pool/src/bev_pool_triton.py:12-48, 219-227
+# ---------------------------------------------------------------------------
+def check_inputs(feats, coords, B, D, H, W) -> None:
+    """``bev_pool_triton.py:12-31``: shape / dtype / size validation."""
+    if feats.dim() != 2:
+        raise ValueError('feats must have shape [N, C].')
+    if coords.dim() != 2 or coords.size(-1) != 4:
+        raise ValueError('coords must have shape [N, 4].')
+    if feats.size(0) != coords.size(0):
+        raise ValueError('feats and coords must have the same number of points.')
+    if coords.dtype not in (torch.int32, torch.int64):
+        raise TypeError('coords must have dtype torch.int32 or torch.int64.')
+    if feats.dtype not in (torch.float16, torch.float32, torch.bfloat16):
+        raise TypeError('feats must have dtype torch.float16, torch.float32, or torch.bfloat16.')
+    if min(B, D, H, W) <= 0:
+        raise ValueError('B, D, H, W must be positive integers.')
+
+
+def flatten_ranks(coords, B, D, H, W):
+    """``bev_pool_triton.py:34-39``: rank = ((b*D + z)*H + x)*W + y in int64."""
+    x = coords[:, 0].long()
+    y = coords[:, 1].long()
+    z = coords[:, 2].long()
+    b = coords[:, 3].long()
+    return ((b * D + z) * H + x) * W + y
+
+
+def bev_pool_cpu(feats, coords, B, D, H, W):
+    """``bev_pool_triton.py:42-48``: zeros + index_add_ (sequential in point
+    order per cell) -> (B, D, H, W, C)."""
+    ranks = flatten_ranks(coords, B, D, H, W)
+    out = feats.new_zeros((B * D * H * W, feats.size(1)))
+    out.index_add_(0, ranks, feats)
+    return out.view(B, D, H, W, feats.size(1))
+
+
+def bev_pool(feats, coords, B, D, H, W):
+    """``bev_pool_triton.py:219-227`` (CPU branch): checks, fallback, then the
+    ``permute(0, 4, 1, 2, 3).contiguous()`` to (B, C, D, H, W)."""
+    B, D, H, W = int(B), int(D), int(H), int(W)
+    check_inputs(feats, coords, B, D, H, W)
+    out = bev_pool_cpu(feats, coords, B, D, H, W)
+    return out.permute(0, 4, 1, 2, 3).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# models/vtransforms/base.py:131-165
+# ---------------------------------------------------------------------------
+class Quantized(NamedTuple):
+    coords: torch.Tensor  # (N_all, 4) int64 (x, y, z, b), before the kept mask
+    kept: torch.Tensor  # (N_all,) bool
+
+
+def quantize(geom_feats, dx, bx, nx) -> Quantized:
+    """``base.py:139-156``: ((g - (bx - dx/2)) / dx).long() in fp32, batch
+    index appended as column 3 (batch-major point order), kept mask
+    0 <= q_k < nx[k]."""
+    B = geom_feats.shape[0]
+    n_per_batch = geom_feats[0].numel() // 3
+    q = ((geom_feats - (bx - dx / 2.0)) / dx).long()
+    q = q.reshape(-1, 3)
+    batch_ix = torch.arange(B, dtype=torch.long).repeat_interleave(n_per_batch).view(-1, 1)
+    coords = torch.cat((q, batch_ix), 1)
+    kept = (
+        (coords[:, 0] >= 0)
+        & (coords[:, 0] < nx[0])
+        & (coords[:, 1] >= 0)
+        & (coords[:, 1] < nx[1])
+        & (coords[:, 2] >= 0)
+        & (coords[:, 2] < nx[2])
+    )
+    return Quantized(coords, kept)
+
+
+def lss_bev_pool(geom_feats, x, dx, bx, nx):
+    """``base.py:131-165`` with ``force_fp32`` (``models/helper/amp.py:35-67``):
+    flatten x to (N_all, C), quantise, keep in-bounds points (order-preserving
+    boolean gather), bev_pool to (B, C, Dz, H, W), collapse Z by
+    ``cat(unbind(2), 1)`` -> (B, C*Dz, H, W).  Differentiable in x."""
+    x = x.float()
+    geom_feats = geom_feats.float()
+    B, N, D, H, W, C = x.shape
+    xf = x.reshape(B * N * D * H * W, C)
+    q = quantize(geom_feats, dx, bx, nx)
+    xk = xf[q.kept]
+    ck = q.coords[q.kept]
+    out = bev_pool(xk, ck, B, int(nx[2]), int(nx[0]), int(nx[1]))
+    return torch.cat(out.unbind(dim=2), 1)
+
+
+# ---------------------------------------------------------------------------
+# sort permutation and intervals (ops/bev_pool/bev_pool_legacy.py:56-61,
+# 102-104) on the (b, z, x, y) ranks of the kept points
+# ---------------------------------------------------------------------------
+def sort_perm(ranks):
+    """Stable argsort of the ranks: the permutation a sequential per-cell sum
+    in point order visits (``bev_pool_legacy.py:103`` made stable)."""
+    return torch.sort(ranks, stable=True).indices
+
+
+def intervals(sorted_ranks):
+    """``bev_pool_legacy.py:56-61``: starts where r[i] != r[i-1] (int32),
+    lengths by difference with the last one n - start."""
+    n = sorted_ranks.shape[0]
+    if n == 0:
+        return torch.zeros(0, dtype=torch.int32), torch.zeros(0, dtype=torch.int32)
+    kept = torch.ones(n, dtype=torch.bool)
+    kept[1:] = sorted_ranks[1:] != sorted_ranks[:-1]
+    starts = torch.where(kept)[0].int()
+    lengths = torch.zeros_like(starts)
+    lengths[:-1] = starts[1:] - starts[:-1]
+    lengths[-1] = n - starts[-1]
+    return starts, lengths
+
+
+def backward_gather(grad, coords, B, D, H, W):
+    """Gradient of ``bev_pool`` w.r.t. feats: index_add_'s backward is
+    ``grad.index_select(0, ranks)`` on the (B*D*H*W, C) view of the
+    channel-last gradient (``bev_pool_triton.py:102-150`` computes the same
+    gather)."""
+    ranks = flatten_ranks(coords, B, D, H, W)
+    g = grad.permute(0, 2, 3, 4, 1).reshape(B * D * H * W, grad.shape[1])
+    return g.index_select(0, ranks)
+
+
+class LSSIndex(NamedTuple):
+    rank: torch.Tensor  # (N_all,) int64, -1 for dropped points
+    kept: torch.Tensor  # (N_all,) bool
+    perm: torch.Tensor  # (N_kept,) int64 original point index, in sorted order
+    sorted_ranks: torch.Tensor  # (N_kept,) int64
+    starts: torch.Tensor  # (n_int,) int32
+    lengths: torch.Tensor  # (n_int,) int32
+
+
+def lss_index(geom_feats, dx, bx, nx) -> LSSIndex:
+    """Every index-stage quantity of the vtransform path, in original point
+    indices: rank (-1 dropped), kept mask, the stable sort permutation of the
+    kept points, their sorted ranks and the interval starts/lengths."""
+    q = quantize(geom_feats.float(), dx, bx, nx)
+    B = geom_feats.shape[0]
+    ranks = flatten_ranks(q.coords, B, int(nx[2]), int(nx[0]), int(nx[1]))
+    rank = torch.where(q.kept, ranks, torch.full_like(ranks, -1))
+    kept_idx = torch.nonzero(q.kept).squeeze(1)
+    rk = ranks[kept_idx]
+    order = sort_perm(rk)
+    perm = kept_idx[order]
+    sorted_ranks = rk[order]
+    starts, lengths = intervals(sorted_ranks)
+    return LSSIndex(rank, q.kept, perm, sorted_ranks, starts, lengths)

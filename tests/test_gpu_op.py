@@ -1,0 +1,208 @@
+"""GPU parity of the op-level ``bev_pool(feats, coords, B, D, H, W)`` (through
+the C ABI) against the CPU oracle (oracle/torch_fallback.py).
+
+Bar: indices (ranks, stable permutation, interval starts/lengths) and fp32
+forward/backward bit-exact; fp16/bf16 forward bit-exact against the fp32
+sequential sum rounded once (fp32 accumulation) and within 1e-2 relative of
+the fp32 reference; fp16/bf16 backward bit-exact (a copy).
+"""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import torch_fallback as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def rand_case(N, C, B, D, H, W, dtype=torch.float32, seed=0, idx_dtype=torch.int32):
+    """The reference's _build_case_tensors (tests/test_ops/test_bev_pool.py:24-47),
+    generated on the CPU with a seeded generator."""
+    g = torch.Generator().manual_seed(seed)
+    feats = torch.randn((N, C), generator=g).to(dtype)
+    coords = torch.stack([
+        torch.randint(0, H, (N,), generator=g), torch.randint(0, W, (N,), generator=g),
+        torch.randint(0, D, (N,), generator=g), torch.randint(0, B, (N,), generator=g),
+    ], 1).to(idx_dtype)
+    return feats, coords
+
+
+def bits(t):
+    t = t.detach().cpu().contiguous()
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+def assert_bit_equal(a, b, what=''):
+    assert a.shape == b.shape, (what, a.shape, b.shape)
+    assert a.dtype == b.dtype, (what, a.dtype, b.dtype)
+    if not torch.equal(bits(a), bits(b)):
+        d = (a.detach().cpu().double() - b.detach().cpu().double()).abs()
+        raise AssertionError(f'{what}: not bit-identical (max |diff| {d.max().item():.3e}, '
+                             f'{int((bits(a) != bits(b)).sum())} elements)')
+
+
+def run_op(pkg, feats, coords, sizes, cuda, upstream=None):
+    f = feats.to(cuda).requires_grad_(True)
+    out = pkg.bev_pool(f, coords.to(cuda), *sizes)
+    if upstream is None:
+        upstream = torch.randn(out.shape, generator=torch.Generator().manual_seed(11))
+    (out * upstream.to(cuda, out.dtype)).sum().backward()
+    torch.cuda.synchronize()
+    return out, f.grad, upstream
+
+
+def oracle_op(feats, coords, sizes, upstream):
+    f = feats.clone().requires_grad_(True)
+    out = ref.bev_pool(f, coords, *sizes)
+    (out * upstream.to(out.dtype)).sum().backward()
+    return out, f.grad
+
+
+def test_known_case(pkg, cuda):
+    k = json.loads((GOLDEN / 'known_case.json').read_text())
+    feats = torch.tensor(k['feats'], device=cuda)
+    coords = torch.tensor(k['coords'], dtype=torch.int32, device=cuda)
+    out = pkg.bev_pool(feats, coords, k['B'], k['D'], k['H'], k['W'])
+    assert out.is_contiguous() and list(out.shape) == k['expected_shape']
+    assert torch.equal(out.cpu(), torch.tensor(k['expected']))
+
+
+def test_known_case_rejects(pkg, cuda):
+    k = json.loads((GOLDEN / 'known_case.json').read_text())
+    for case in k['reject']:
+        feats = torch.zeros((4, 3), dtype=getattr(torch, case['feats_dtype']), device=cuda)
+        coords = torch.zeros((4, 4), dtype=getattr(torch, case['coords_dtype']), device=cuda)
+        with pytest.raises(TypeError):
+            pkg.bev_pool(feats, coords, 1, 1, 1, 1)
+
+
+def test_order_case(pkg, cuda):
+    o = json.loads((GOLDEN / 'order_case.json').read_text())
+    feats = torch.from_numpy(np.array(o['feats_f32_bits'], np.uint32).view(np.float32).copy())
+    coords = torch.tensor(o['coords'], dtype=torch.int64)
+    out = pkg.bev_pool(feats.to(cuda), coords.to(cuda), o['B'], o['D'], o['H'], o['W'])
+    got = out.cpu().reshape(-1).view(torch.int32).numpy().astype(np.uint32).tolist()
+    assert got == o['expected_f32_bits']
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+def test_reference_parity_case(pkg, cuda, dtype):
+    """The reference's legacy-vs-Triton case (test_bev_pool.py:87-119):
+    B,D,H,W = 2,3,4,5, N=64, C=8, seed 0, random upstream gradient."""
+    sizes = (2, 3, 4, 5)
+    feats, coords = rand_case(64, 8, *sizes, dtype=dtype)
+    out, grad, up = run_op(pkg, feats, coords, sizes, cuda)
+    out32, grad32 = oracle_op(feats.float(), coords, sizes, up)
+    assert out.dtype == dtype and out.is_contiguous()
+    if dtype == torch.float32:
+        assert_bit_equal(out, out32, 'fwd')
+        assert_bit_equal(grad, grad32, 'bwd')
+    else:
+        assert_bit_equal(out, out32.to(dtype), 'fwd (fp32 accumulation, one rounding)')
+        rel = (out.cpu().float() - out32).norm() / out32.norm()
+        assert rel <= 1e-2, rel
+        # backward: a copy of the (dtype-rounded) upstream gradient
+        _, gref = oracle_op(feats, coords, sizes, up)
+        assert_bit_equal(grad, gref, 'bwd')
+
+
+@pytest.mark.parametrize('idx_dtype', [torch.int32, torch.int64])
+def test_index_stage_bit_exact(pkg, cuda, idx_dtype):
+    sizes = (2, 3, 17, 19)
+    _, coords = rand_case(20000, 1, *sizes, seed=3, idx_dtype=idx_dtype)
+    exp = pkg.BevPoolIndexExport(coords.to(cuda), *sizes)
+    ranks = ref.flatten_ranks(coords, *sizes)
+    assert torch.equal(exp.rank.cpu(), ranks)
+    perm = ref.sort_perm(ranks)
+    assert torch.equal(exp.perm.cpu(), perm)
+    assert torch.equal(exp.sorted_ranks.cpu(), ranks[perm])
+    starts, lengths = ref.intervals(ranks[perm])
+    assert torch.equal(exp.starts.cpu(), starts)
+    assert torch.equal(exp.lengths.cpu(), lengths)
+    assert torch.equal(exp.cells.cpu().long(), ranks[perm][starts.long()])
+    assert exp.n_bad == 0
+
+
+@pytest.mark.parametrize('N,sizes,C', [
+    (0, (1, 1, 2, 3), 4),           # empty input -> zeros
+    (1, (1, 1, 1, 1), 1),           # single point, single cell
+    (30000, (1, 1, 1, 1), 5),       # every point in one cell: one 30000-long interval
+    (5000, (3, 2, 7, 300), 3),      # C not a multiple of 4, >10-bit ranks (2 radix passes)
+    (4000, (1, 1, 40, 50), 300),    # C > 256 (channel blocking)
+    (70000, (2, 4, 64, 64), 16),    # 15-bit ranks
+])
+def test_shapes_and_edges(pkg, cuda, N, sizes, C):
+    feats, coords = rand_case(N, C, *sizes, seed=N + C)
+    out, grad, up = run_op(pkg, feats, coords, sizes, cuda)
+    out32, grad32 = oracle_op(feats, coords, sizes, up)
+    assert_bit_equal(out, out32, 'fwd')
+    assert_bit_equal(grad, grad32, 'bwd')
+
+
+def test_large_rank_space(pkg, cuda):
+    """2^21 cells: three radix passes."""
+    sizes = (2, 1, 1024, 1024)
+    feats, coords = rand_case(50000, 4, *sizes, seed=9)
+    out, grad, up = run_op(pkg, feats, coords, sizes, cuda)
+    out32, grad32 = oracle_op(feats, coords, sizes, up)
+    assert_bit_equal(out, out32, 'fwd')
+    assert_bit_equal(grad, grad32, 'bwd')
+
+
+def test_noncontiguous_feats(pkg, cuda):
+    sizes = (1, 2, 9, 11)
+    feats, coords = rand_case(3000, 12, *sizes, seed=4)
+    wide = torch.randn(3000, 30)
+    wide[:, 5:17] = feats
+    f = wide.to(cuda)[:, 5:17]  # row stride 30, channel stride 1
+    assert not f.is_contiguous()
+    out = pkg.bev_pool(f, coords.to(cuda), *sizes)
+    assert_bit_equal(out, ref.bev_pool(feats, coords, *sizes), 'fwd strided rows')
+    ft = feats.t().contiguous().to(cuda).t()  # channel stride != 1
+    out = pkg.bev_pool(ft, coords.to(cuda), *sizes)
+    assert_bit_equal(out, ref.bev_pool(feats, coords, *sizes), 'fwd transposed view')
+
+
+def test_signed_zero_and_specials(pkg, cuda):
+    sizes = (1, 1, 2, 2)
+    feats = torch.tensor([[-0.0, 1.0], [float('inf'), -0.0], [1.0, float('nan')],
+                          [-0.0, -0.0]])
+    coords = torch.tensor([[0, 0, 0, 0], [0, 1, 0, 0], [0, 1, 0, 0], [1, 1, 0, 0]])
+    out = pkg.bev_pool(feats.to(cuda), coords.to(cuda), *sizes)
+    exp = ref.bev_pool(feats, coords, *sizes)
+    assert_bit_equal(out, exp, 'fwd specials')
+
+
+def test_out_of_range_coords_raise(pkg, cuda):
+    feats, coords = rand_case(100, 3, 1, 2, 3, 4, seed=1)
+    coords[17] = torch.tensor([3, 0, 0, 0], dtype=torch.int32)  # x == H
+    with pytest.raises(RuntimeError, match='out of bounds'):
+        pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
+    coords[17] = torch.tensor([0, 0, 0, -1], dtype=torch.int32)  # negative batch
+    with pytest.raises(RuntimeError, match='out of bounds'):
+        pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
+    # a rank inside [0, B*D*H*W) is accepted even if one coordinate is out of
+    # range: the reference flattens first (x = -1, y = 5 -> (-1)*4 + 5 = 1)
+    coords[17] = torch.tensor([-1, 5, 0, 0], dtype=torch.int32)
+    out = pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
+    assert_bit_equal(out, ref.bev_pool(feats, coords, 1, 2, 3, 4), 'flattened-rank semantics')
+
+
+def test_deterministic(pkg, cuda):
+    sizes = (1, 1, 40, 40)
+    feats, coords = rand_case(100000, 20, *sizes, seed=8)
+    f, c = feats.to(cuda), coords.to(cuda)
+    a = pkg.bev_pool(f, c, *sizes)
+    b = pkg.bev_pool(f, c, *sizes)
+    assert torch.equal(bits(a), bits(b))
+
+
+def test_zero_channels(pkg, cuda):
+    out = pkg.bev_pool(torch.zeros(5, 0, device=cuda), torch.zeros(5, 4, dtype=torch.int32,
+                                                                    device=cuda), 1, 1, 1, 1)
+    assert out.shape == (1, 0, 1, 1, 1)

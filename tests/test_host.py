@@ -1,0 +1,149 @@
+"""CPU tests of the host side: the C ABI library loads and exports every
+symbol include/bevpool.h declares, argument validation returns the documented
+status codes (these calls fail before any HIP call, so no GPU is needed), and
+the Python surface mirrors the reference's checks and exception types."""
+from __future__ import annotations
+
+import json
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, ROOT
+
+HEADER = ROOT / 'include' / 'bevpool.h'
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(bevpool_\w+)\s*\(', text)))
+
+
+def test_header_and_binding_agree(pkg):
+    from bevfusion_triton_amd import _lib
+
+    assert header_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.library()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert lib.bevpool_abi_version() == 1
+    assert lib.bevpool_last_error() == b''
+
+
+def test_workspace_sizes(pkg):
+    lib = pkg.library()
+    small = lib.bevpool_index_workspace_bytes(1000, 100)
+    big = lib.bevpool_index_workspace_bytes(2_000_000, 129600)
+    assert 0 < small < big
+    assert big >= 2_000_000 * 8  # ping-pong key buffer
+    assert big % 256 == 0
+    assert lib.bevpool_forward_scratch_bytes(129600, 80) == 129600 * 80 * 4
+    assert lib.bevpool_backward_scratch_bytes(129600, 80, 2) == 129600 * 80 * 2
+
+
+def test_status_codes_without_gpu(pkg):
+    from bevfusion_triton_amd import _lib
+
+    lib = pkg.library()
+    meta = np.zeros(8, np.int32)
+    ws = np.zeros(1 << 16, np.uint8)
+    # unsupported dtype code
+    st = lib.bevpool_forward(None, 7, 1, 1, 0, None, None, None, None, 1, 1, 1, 1, 1, 1, None,
+                             None, 0, None)
+    assert st == -1 and b'dtype' in lib.bevpool_last_error()
+    # B*D*H*W out of range
+    st = lib.bevpool_sort(None, 0, 0, None, None, None, meta.ctypes.data, ws.ctypes.data,
+                          ws.size, None)
+    assert st == -1 and b'B*D*H*W' in lib.bevpool_last_error()
+    # workspace too small
+    st = lib.bevpool_sort(meta.ctypes.data, 100000, 10, None, None, None, meta.ctypes.data,
+                          ws.ctypes.data, 16, None)
+    assert st == -3 and b'workspace' in lib.bevpool_last_error()
+    # non-positive grid
+    st = lib.bevpool_coord_ranks(None, 4, 0, 4, 1, 0, 1, 1, None, meta.ctypes.data,
+                                 ws.ctypes.data, ws.size, None)
+    assert st == -1
+    # coords element size
+    st = lib.bevpool_coord_ranks(None, 2, 0, 4, 1, 1, 1, 1, None, meta.ctypes.data,
+                                 ws.ctypes.data, ws.size, None)
+    assert st == -1 and b'coord_bytes' in lib.bevpool_last_error()
+    with pytest.raises(_lib.BevPoolError, match='status -1'):
+        _lib.check(lib.bevpool_forward(None, 7, 1, 1, 0, None, None, None, None, 1, 1, 1, 1, 1,
+                                       1, None, None, 0, None), 'bevpool_forward')
+
+
+def test_op_level_checks_mirror_reference(pkg):
+    k = json.loads((GOLDEN / 'known_case.json').read_text())
+    for case in k['reject']:
+        feats = torch.zeros((4, 3), dtype=getattr(torch, case['feats_dtype']))
+        coords = torch.zeros((4, 4), dtype=getattr(torch, case['coords_dtype']))
+        with pytest.raises(TypeError):
+            pkg.bev_pool(feats, coords, 1, 1, 1, 1)
+    with pytest.raises(ValueError, match=r'feats must have shape \[N, C\]'):
+        pkg.bev_pool(torch.zeros(4), torch.zeros(4, 4, dtype=torch.int32), 1, 1, 1, 1)
+    with pytest.raises(ValueError, match=r'coords must have shape \[N, 4\]'):
+        pkg.bev_pool(torch.zeros(4, 3), torch.zeros(4, 3, dtype=torch.int32), 1, 1, 1, 1)
+    with pytest.raises(ValueError, match='same number of points'):
+        pkg.bev_pool(torch.zeros(4, 3), torch.zeros(5, 4, dtype=torch.int32), 1, 1, 1, 1)
+    with pytest.raises(ValueError, match='positive'):
+        pkg.bev_pool(torch.zeros(4, 3), torch.zeros(4, 4, dtype=torch.int32), 1, 0, 1, 1)
+    # 0-d integer tensors are accepted for the sizes (the vtransform passes nx[k])
+    with pytest.raises(ValueError, match='positive'):
+        pkg.bev_pool(torch.zeros(4, 3), torch.zeros(4, 4, dtype=torch.int32), torch.tensor(1),
+                     torch.tensor(0), torch.tensor(1), torch.tensor(1))
+
+
+def test_no_cpu_fallback(pkg):
+    k = json.loads((GOLDEN / 'known_case.json').read_text())
+    feats = torch.tensor(k['feats'])
+    coords = torch.tensor(k['coords'], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match='no CPU fallback'):
+        pkg.bev_pool(feats, coords, 1, 1, 2, 1)
+    geom = torch.zeros(1, 1, 1, 1, 2, 3)
+    x = torch.zeros(1, 1, 1, 1, 2, 4)
+    with pytest.raises(RuntimeError, match='no CPU fallback'):
+        pkg.lss_bev_pool(geom, x, *pkg.gen_dx_bx((-1, 1, 1), (-1, 1, 1), (-1, 1, 2)))
+
+
+def test_gen_dx_bx_matches_reference_restatement(pkg):
+    from oracle import torch_fallback as ref
+
+    for bounds in [((-54.0, 54.0, 0.3), (-54.0, 54.0, 0.3), (-10.0, 10.0, 20.0)),
+                   ((-51.2, 51.2, 0.4), (-51.2, 51.2, 0.4), (-10.0, 10.0, 20.0)),
+                   ((-54.0, 54.0, 0.15), (-54.0, 54.0, 0.15), (-10.0, 10.0, 20.0))]:
+        for a, b in zip(pkg.gen_dx_bx(*bounds), ref.gen_dx_bx(*bounds)):
+            assert a.dtype == b.dtype and torch.equal(a, b)
+
+
+def test_host_grid_offset_bits(pkg):
+    q = json.loads((GOLDEN / 'quantize_edges.json').read_text())['grid']
+    offset, dx, nx = pkg.host_grid(*pkg.gen_dx_bx(q['xbound'], q['ybound'], q['zbound']))
+    assert offset.view(np.uint32).tolist() == q['offset_f32_bits']
+    assert dx.view(np.uint32).tolist() == q['dx_f32_bits']
+    assert nx == q['nx']
+
+
+def test_transform_module_grid_cache(pkg):
+    m = pkg.BevPoolTransform((-54.0, 54.0, 0.3), (-54.0, 54.0, 0.3), (-10.0, 10.0, 20.0))
+    g0 = m.grid()
+    assert g0[2] == [360, 360, 1]
+    with torch.no_grad():
+        m.dx.mul_(2.0)  # in-place change is picked up
+    assert m.grid()[1][0] == np.float32(0.6)
+
+
+def test_synthetic_rig_shapes(pkg):
+    from bevfusion_triton_amd import synthetic
+
+    spec = synthetic.CASES['det']
+    geom = synthetic.make_geometry(spec)
+    assert geom.shape == (1, 6, 118, 32, 88, 3)
+    assert geom[..., 0].numel() == 1_993_728
+    # cameras 1.5 m high: the nearest depth bin lies within a few metres
+    assert torch.isfinite(geom).all()
