@@ -586,6 +586,208 @@ __global__ __launch_bounds__(kThreads) void accum_rows_kernel(
   }
 }
 
+// ---- software-pipelined forward accumulation (16-byte rows) ---------------
+//
+// Same ownership as accum_rows_kernel (block b owns the sorted positions
+// [snap(b*P), snap((b+1)*P)), whole cells only), restructured so that memory
+// latency is hidden inside the block:
+//   * the range is cut into stages of kStageRows sorted points; a stage's
+//     rows are gathered with 16-byte loads (slot i of thread t covers row
+//     (t + 256 i) / rowq, 16-byte column (t + 256 i) % rowq) into registers;
+//   * two stages are in flight while a third is accumulated from LDS: loads
+//     of stage k+2 and the point indices of stage k+3 are issued before stage
+//     k is summed, stage k+1 is written to LDS after it; one barrier a stage;
+//   * the channels are spread over the four waves (wave w, lane l owns channel
+//     w*ceil(C/4) + l), each lane adding its column of the stage in order into
+//     one fp32 accumulator; a cell's sum is stored to acc when the next cell
+//     starts (start flags from a ballot over the stage's ranks) or the range
+//     ends, so a cell spanning stages keeps one sequential chain.
+constexpr int kStageRows = 64;
+
+// native 16-byte vector (register-promotable, unlike the HIP u32x4 wrapper)
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Point indices of one stage.  Every slot is loaded (straight-line code keeps
+// the compiler's vmcnt accounting exact): slots past the stage's rows repeat
+// its last row, and a stage past the range end reads the range's first row.
+template <int kSlots>
+__device__ __forceinline__ void stage_index(const uint32_t *__restrict__ kw, int64_t base,
+                                            int rowq, int rows, int64_t first,
+                                            uint32_t (&idx)[kSlots]) {
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const int slot = int(threadIdx.x) + kThreads * i;
+    int r = slot / rowq;
+    r = r < rows - 1 ? r : rows - 1;
+    idx[i] = kw[2 * (rows > 0 ? base + r : first)];  // low word: point index
+  }
+}
+
+template <int kSlots>
+__device__ __forceinline__ void stage_load(const char *__restrict__ xb, int64_t ld_bytes,
+                                           int col_bytes, int rowq,
+                                           const uint32_t (&idx)[kSlots], u32x4 (&d)[kSlots]) {
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const int slot = int(threadIdx.x) + kThreads * i;
+    const int q = slot - (slot / rowq) * rowq;
+    d[i] = *reinterpret_cast<const u32x4 *>(xb + int64_t(idx[i]) * ld_bytes + col_bytes +
+                                             q * 16);
+  }
+}
+
+// Sorted position whose rank thread t (< kStageRows) stages for stage k:
+// row t of the stage, clamped into the range like stage_index.
+__device__ __forceinline__ int64_t stage_row_pos(int64_t s, int64_t e, int k) {
+  const int64_t b = s + int64_t(k) * kStageRows;
+  if (b >= e) return s;
+  const int64_t p = b + (threadIdx.x & (kStageRows - 1));
+  return p < e ? p : e - 1;
+}
+
+template <int kSlots>
+__device__ __forceinline__ void stage_store(u32x4 *__restrict__ lbuf, int rowq, int rows,
+                                            const u32x4 (&d)[kSlots]) {
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const int slot = int(threadIdx.x) + kThreads * i;
+    if (slot < rows * rowq) lbuf[slot] = d[i];
+  }
+}
+
+template <typename T>
+struct PipeAcc {
+  float a = 0.0f;  // running sum of the current cell (this lane's channel)
+  int cur = -1;    // rank of the current cell
+  int carry = -1;  // rank of the previous stage's last row
+
+  // Adds the `rows` rows of one LDS stage, in order.
+  __device__ __forceinline__ void add_stage(const typename T::raw *__restrict__ lb,
+                                            const int *__restrict__ lrk, int rows, int cb,
+                                            int rd_c, bool acc_lane, float *__restrict__ out,
+                                            int64_t row_elems) {
+    const int lane = lane_id();
+    const int rkl = lane < rows ? lrk[lane] : -1;
+    int prev = __shfl_up(rkl, 1, 64);
+    if (lane == 0) prev = carry;
+    const uint64_t starts = __ballot(lane < rows && rkl != prev);
+    if (rows > 0) carry = __builtin_amdgcn_readlane(rkl, rows - 1);
+    for (int j0 = 0; j0 < rows; j0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = T::load(lb + (j0 + u) * cb + rd_c);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u;
+        if (j < rows) {
+          if ((starts >> j) & 1) {
+            if (cur >= 0 && acc_lane) out[int64_t(cur) * row_elems] = a;
+            a = 0.0f;
+            cur = __builtin_amdgcn_readlane(rkl, j);
+          }
+          a += v[u];
+        }
+      }
+    }
+  }
+};
+
+// One pipeline step.  On entry the loads still in flight are, in issue order,
+// the point indices of stage k+2 (idx_cur), then the rows and ranks of stage
+// k+1 (d_nxt, rk_nxt); stage k is in cur_buf.  Issuing the indices of stage
+// k+3 before the rows of stage k+2 keeps that order, so waiting for idx_cur
+// never waits for the rows of stage k+1 (vmcnt retires in issue order).
+template <typename T, int kSlots>
+__device__ __forceinline__ void pipe_step(
+    int k, int nst, int64_t s, int64_t e, const char *__restrict__ xb, int64_t ld_bytes,
+    int col_bytes, int rowq, int cb, int rd_c, bool acc_lane, const uint32_t *__restrict__ kw,
+    const uint32_t (&idx_cur)[kSlots], uint32_t (&idx_nxt)[kSlots], u32x4 *__restrict__ cur_buf,
+    int *__restrict__ cur_rk, u32x4 (&d_cur)[kSlots], int &rk_cur, u32x4 *__restrict__ nxt_buf,
+    int *__restrict__ nxt_rk, const u32x4 (&d_nxt)[kSlots], const int &rk_nxt, PipeAcc<T> &st,
+    float *__restrict__ out, int64_t row_elems) {
+  auto rows_of = [&](int kk) -> int {
+    const int64_t b = s + int64_t(kk) * kStageRows;
+    return b >= e ? 0 : int(e - b < kStageRows ? e - b : kStageRows);
+  };
+  // stage k+3: its point indices
+  stage_index(kw, s + int64_t(k + 3) * kStageRows, rowq, rows_of(k + 3), s, idx_nxt);
+  // stage k+2: gather its rows and ranks
+  stage_load(xb, ld_bytes, col_bytes, rowq, idx_cur, d_cur);
+  rk_cur = kw[2 * stage_row_pos(s, e, k + 2) + 1];
+  // stage k: sum it
+  st.add_stage(reinterpret_cast<const typename T::raw *>(cur_buf), cur_rk, rows_of(k), cb, rd_c,
+               acc_lane, out, row_elems);
+  // stage k+1: into the other LDS buffer (its old contents were summed in step k-1)
+  if (k + 1 < nst) {
+    stage_store(nxt_buf, rowq, rows_of(k + 1), d_nxt);
+    if (threadIdx.x < kStageRows) nxt_rk[threadIdx.x] = rk_nxt;
+  }
+  __syncthreads();
+}
+
+template <typename T, int kSlots>
+__global__ __launch_bounds__(kThreads) void accum_pipe_kernel(
+    const char *__restrict__ xb, int64_t ld_bytes, int C, int CB,
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
+    const int32_t *__restrict__ cend, float *__restrict__ acc, int64_t P) {
+  using raw = typename T::raw;
+  extern __shared__ u32x4 smem4[];
+  const int rowq_max = CB * int(sizeof(raw)) / 16;
+  u32x4 *buf0 = smem4;
+  u32x4 *buf1 = smem4 + kStageRows * rowq_max;
+  int *rk0s = reinterpret_cast<int *>(smem4 + 2 * kStageRows * rowq_max);
+  int *rk1s = rk0s + kStageRows;
+  const uint32_t *kw = reinterpret_cast<const uint32_t *>(keys);
+
+  const int64_t n = meta[BEVPOOL_META_N_KEPT];
+  const int64_t r0 = int64_t(blockIdx.x) * P;
+  if (r0 >= n) return;
+  const int64_t s = snap_to_cell(r0, n, keys, cend);
+  const int64_t e = snap_to_cell(r0 + P < n ? r0 + P : n, n, keys, cend);
+  if (s >= e) return;
+  const int nst = int((e - s + kStageRows - 1) / kStageRows);
+  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
+  auto rows_of = [&](int kk) -> int {
+    const int64_t b = s + int64_t(kk) * kStageRows;
+    return b >= e ? 0 : int(e - b < kStageRows ? e - b : kStageRows);
+  };
+
+  for (int c0 = 0; c0 < C; c0 += CB) {
+    const int cb = C - c0 < CB ? C - c0 : CB;
+    const int rowq = cb * int(sizeof(raw)) / 16;
+    const int cpw = (cb + kWaves - 1) / kWaves;
+    const int my_c = w * cpw + lane;
+    const bool acc_lane = lane < cpw && my_c < cb;
+    const int rd_c = acc_lane ? my_c : 0;
+    const int col_bytes = c0 * int(sizeof(raw));
+    float *out = acc + c0 + my_c;
+
+    uint32_t ia[kSlots], ib[kSlots];
+    u32x4 d0[kSlots], d1[kSlots];
+    int rk0 = -1, rk1 = -1;
+    // prologue: leave in flight, in order, indices(2) then rows(1); stage 0 in LDS
+    stage_index(kw, s, rowq, rows_of(0), s, ia);
+    stage_index(kw, s + kStageRows, rowq, rows_of(1), s, ib);
+    stage_load(xb, ld_bytes, col_bytes, rowq, ia, d0);
+    rk0 = kw[2 * stage_row_pos(s, e, 0) + 1];
+    stage_index(kw, s + 2 * kStageRows, rowq, rows_of(2), s, ia);
+    stage_load(xb, ld_bytes, col_bytes, rowq, ib, d1);
+    rk1 = kw[2 * stage_row_pos(s, e, 1) + 1];
+    stage_store(buf0, rowq, rows_of(0), d0);
+    if (tid < kStageRows) rk0s[tid] = rk0;
+    __syncthreads();
+
+    PipeAcc<T> st;
+    for (int k = 0; k < nst; k += 2) {  // a step past the last stage sums nothing
+      pipe_step<T, kSlots>(k, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, rd_c, acc_lane, kw,
+                           ia, ib, buf0, rk0s, d0, rk0, buf1, rk1s, d1, rk1, st, out, C);
+      pipe_step<T, kSlots>(k + 1, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, rd_c, acc_lane,
+                           kw, ib, ia, buf1, rk1s, d1, rk1, buf0, rk0s, d0, rk0, st, out, C);
+    }
+    if (st.cur >= 0 && acc_lane) out[int64_t(st.cur) * C] = st.a;
+  }
+}
+
 // acc rows (cell-major fp32) -> out (channel-first, dtype T), tile of 64 cells
 // x 64 channels through LDS; empty cells are written as 0.
 template <typename T>
@@ -762,6 +964,47 @@ int check_index_args(int64_t n_points, int64_t n_cells, const void *rank, const 
 }
 
 size_t dtype_size(int32_t dtype) { return dtype == BEVPOOL_F32 ? 4 : 2; }
+
+template <typename T>
+int launch_accum_pipe_t(int slots, unsigned grid, size_t smem, hipStream_t s, const char *x,
+                        int64_t ld_bytes, int C, int CB, const uint64_t *keys,
+                        const int32_t *meta, const int32_t *cend, float *acc) {
+#define BEVPOOL_PIPE_CASE(K)                                                                   \
+  case K:                                                                                      \
+    hipLaunchKernelGGL((accum_pipe_kernel<T, K>), dim3(grid), dim3(kThreads), smem, s, x,      \
+                       ld_bytes, C, CB, keys, meta, cend, acc, kRangePoints);                  \
+    break;
+  switch (slots) {
+    BEVPOOL_PIPE_CASE(1)
+    BEVPOOL_PIPE_CASE(2)
+    BEVPOOL_PIPE_CASE(3)
+    BEVPOOL_PIPE_CASE(4)
+    BEVPOOL_PIPE_CASE(5)
+    BEVPOOL_PIPE_CASE(6)
+    BEVPOOL_PIPE_CASE(7)
+    BEVPOOL_PIPE_CASE(8)
+    default:
+      return fail(BEVPOOL_EINVAL, "internal: %d slots per thread", slots);
+  }
+#undef BEVPOOL_PIPE_CASE
+  return check_launch("accum_pipe");
+}
+
+int launch_accum_pipe(int32_t dtype, int slots, unsigned grid, size_t smem, hipStream_t s,
+                      const char *x, int64_t ld_bytes, int C, int CB, const uint64_t *keys,
+                      const int32_t *meta, const int32_t *cend, float *acc) {
+  switch (dtype) {
+    case BEVPOOL_F32:
+      return launch_accum_pipe_t<F32>(slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend,
+                                      acc);
+    case BEVPOOL_F16:
+      return launch_accum_pipe_t<F16>(slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend,
+                                      acc);
+    default:
+      return launch_accum_pipe_t<BF16>(slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta,
+                                       cend, acc);
+  }
+}
 
 }  // namespace
 
@@ -978,31 +1221,48 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
   float *acc = static_cast<float *>(scratch);
   int st;
   if (n_points > 0) {
-    const int CB = C < kThreads ? C : kThreads;
-    int R = 8192 / CB;
-    if (R > 64) R = 64;
-    if (R < 1) R = 1;
-    const size_t smem = size_t(R) * CB * sizeof(float) + size_t(R + 1) * sizeof(int);
+    const size_t es = dtype_size(dtype);
+    const bool vec16 = (size_t(C) * es) % 16 == 0 && (size_t(feats_row_stride) * es) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(feats) % 16 == 0;
     const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
-    LaunchTimer t("accum_rows", s);
-    switch (dtype) {
-      case BEVPOOL_F32:
-        hipLaunchKernelGGL(accum_rows_kernel<F32>, dim3(grid), dim3(kThreads), smem, s,
-                           static_cast<const uint32_t *>(feats), feats_row_stride, C, CB, R, keys,
-                           meta, cell_end, acc, kRangePoints);
-        break;
-      case BEVPOOL_F16:
-        hipLaunchKernelGGL(accum_rows_kernel<F16>, dim3(grid), dim3(kThreads), smem, s,
-                           static_cast<const uint16_t *>(feats), feats_row_stride, C, CB, R, keys,
-                           meta, cell_end, acc, kRangePoints);
-        break;
-      default:
-        hipLaunchKernelGGL(accum_rows_kernel<BF16>, dim3(grid), dim3(kThreads), smem, s,
-                           static_cast<const uint16_t *>(feats), feats_row_stride, C, CB, R, keys,
-                           meta, cell_end, acc, kRangePoints);
-        break;
+    if (vec16) {
+      // channel block of at most 512 bytes per row: <= 8 16-byte slots per thread per stage
+      const int CBmax = int(512 / es);
+      const int CB = C < CBmax ? C : CBmax;
+      const int rowq = int(size_t(CB) * es / 16);
+      const int slots = (kStageRows * rowq + kThreads - 1) / kThreads;
+      const size_t smem = size_t(2) * kStageRows * rowq * 16 + size_t(2) * kStageRows * sizeof(int);
+      LaunchTimer t("accum_rows", s);
+      st = launch_accum_pipe(dtype, slots, grid, smem, s, static_cast<const char *>(feats),
+                             int64_t(size_t(feats_row_stride) * es), C, CB, keys, meta, cell_end,
+                             acc);
+      if (st) return st;
+    } else {
+      const int CB = C < kThreads ? C : kThreads;
+      int R = 8192 / CB;
+      if (R > 64) R = 64;
+      if (R < 1) R = 1;
+      const size_t smem = size_t(R) * CB * sizeof(float) + size_t(R + 1) * sizeof(int);
+      LaunchTimer t("accum_rows", s);
+      switch (dtype) {
+        case BEVPOOL_F32:
+          hipLaunchKernelGGL(accum_rows_kernel<F32>, dim3(grid), dim3(kThreads), smem, s,
+                             static_cast<const uint32_t *>(feats), feats_row_stride, C, CB, R,
+                             keys, meta, cell_end, acc, kRangePoints);
+          break;
+        case BEVPOOL_F16:
+          hipLaunchKernelGGL(accum_rows_kernel<F16>, dim3(grid), dim3(kThreads), smem, s,
+                             static_cast<const uint16_t *>(feats), feats_row_stride, C, CB, R,
+                             keys, meta, cell_end, acc, kRangePoints);
+          break;
+        default:
+          hipLaunchKernelGGL(accum_rows_kernel<BF16>, dim3(grid), dim3(kThreads), smem, s,
+                             static_cast<const uint16_t *>(feats), feats_row_stride, C, CB, R,
+                             keys, meta, cell_end, acc, kRangePoints);
+          break;
+      }
+      if ((st = check_launch("accum_rows"))) return st;
     }
-    if ((st = check_launch("accum_rows"))) return st;
   }
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
   LaunchTimer t("rows_to_bev", s);

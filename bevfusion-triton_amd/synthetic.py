@@ -153,7 +153,8 @@ def make_features(spec: RigSpec, device='cpu', seed: int = 0) -> torch.Tensor:
     depth = logits.softmax(dim=1)
     # (B*N, D, fH, fW, C) = depth[:, d, h, w] * context[:, c, h, w]
     x = depth.unsqueeze(-1) * context.permute(0, 2, 3, 1).unsqueeze(1)
-    x = x.view(B, N, D, fH, fW, C)
+    # the broadcast product follows its inputs' memory order; force channel-last
+    x = x.contiguous().view(B, N, D, fH, fW, C)
     if spec.dtype != torch.float32:
         x = x.to(spec.dtype)
     return x

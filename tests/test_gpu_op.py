@@ -180,8 +180,9 @@ def test_signed_zero_and_specials(pkg, cuda):
 
 def test_out_of_range_coords_raise(pkg, cuda):
     feats, coords = rand_case(100, 3, 1, 2, 3, 4, seed=1)
-    coords[17] = torch.tensor([3, 0, 0, 0], dtype=torch.int32)  # x == H
-    with pytest.raises(RuntimeError, match='out of bounds'):
+    # x == H at z == D-1: rank ((0*2 + 1)*3 + 3)*4 + 0 = 24 == B*D*H*W
+    coords[17] = torch.tensor([3, 0, 1, 0], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match='index 24 is out of bounds'):
         pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
     coords[17] = torch.tensor([0, 0, 0, -1], dtype=torch.int32)  # negative batch
     with pytest.raises(RuntimeError, match='out of bounds'):
