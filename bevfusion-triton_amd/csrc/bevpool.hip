@@ -655,38 +655,76 @@ __device__ __forceinline__ void stage_store(u32x4 *__restrict__ lbuf, int rowq, 
   }
 }
 
-template <typename T>
+// Channels l, l+64, ... of one LDS row (lane l), widened to fp32.  Columns
+// past the block are clamped to its last channel (read, never stored).  Each
+// channel is a separate 32/16-bit read and a separate scalar add: no 2-wide
+// float vector is ever formed (with packed fp32 ops disabled, hipcc 7.2
+// lowers a <2 x float> add of a 64-bit LDS load to two adds of its low half).
+template <typename T, int kCPL>
+__device__ __forceinline__ void load_channels(const typename T::raw *__restrict__ row,
+                                              const int (&col)[kCPL], float (&v)[kCPL]) {
+#pragma unroll
+  for (int i = 0; i < kCPL; ++i) v[i] = T::load(row + col[i]);
+}
+
+// Per-lane running sums of one wave that owns all the channels of a block:
+// lane l holds channels l + 64 i, i < kCPL.  The stage's rows are walked cell
+// segment by cell segment: the next start bit is found with ctz, the rows of
+// the segment are added in order in a tight loop, and the finished cell is
+// stored when the next one starts.
+template <typename T, int kCPL>
 struct PipeAcc {
-  float a = 0.0f;  // running sum of the current cell (this lane's channel)
+  float a[kCPL];
   int cur = -1;    // rank of the current cell
   int carry = -1;  // rank of the previous stage's last row
 
-  // Adds the `rows` rows of one LDS stage, in order.
+  __device__ __forceinline__ void flush(int cb, float *__restrict__ out, int64_t row_elems) {
+    if (cur >= 0) {
+      float *o = out + int64_t(cur) * row_elems;
+      const int lane = lane_id();
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i)
+        if (lane + 64 * i < cb) o[lane + 64 * i] = a[i];
+    }
+  }
+
   __device__ __forceinline__ void add_stage(const typename T::raw *__restrict__ lb,
                                             const int *__restrict__ lrk, int rows, int cb,
-                                            int rd_c, bool acc_lane, float *__restrict__ out,
-                                            int64_t row_elems) {
+                                            float *__restrict__ out, int64_t row_elems) {
     const int lane = lane_id();
+    int col[kCPL];
+#pragma unroll
+    for (int i = 0; i < kCPL; ++i) col[i] = lane + 64 * i < cb ? lane + 64 * i : cb - 1;
     const int rkl = lane < rows ? lrk[lane] : -1;
     int prev = __shfl_up(rkl, 1, 64);
     if (lane == 0) prev = carry;
     const uint64_t starts = __ballot(lane < rows && rkl != prev);
     if (rows > 0) carry = __builtin_amdgcn_readlane(rkl, rows - 1);
-    for (int j0 = 0; j0 < rows; j0 += 8) {
-      float v[8];
+    int j = 0;
+    while (j < rows) {
+      if ((starts >> j) & 1) {
+        flush(cb, out, row_elems);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = T::load(lb + (j0 + u) * cb + rd_c);
+        for (int i = 0; i < kCPL; ++i) a[i] = 0.0f;
+        cur = __builtin_amdgcn_readlane(rkl, j);
+      }
+      const uint64_t later = j + 1 < 64 ? (starts >> (j + 1)) : 0;
+      int next = later ? j + 1 + int(__builtin_ctzll(later)) : rows;
+      next = next < rows ? next : rows;
+      for (; j + 4 <= next; j += 4) {
+        float v[4][kCPL];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u;
-        if (j < rows) {
-          if ((starts >> j) & 1) {
-            if (cur >= 0 && acc_lane) out[int64_t(cur) * row_elems] = a;
-            a = 0.0f;
-            cur = __builtin_amdgcn_readlane(rkl, j);
-          }
-          a += v[u];
-        }
+        for (int u = 0; u < 4; ++u) load_channels<T, kCPL>(lb + (j + u) * cb, col, v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+      }
+      for (; j < next; ++j) {
+        float v[kCPL];
+        load_channels<T, kCPL>(lb + j * cb, col, v);
+#pragma unroll
+        for (int i = 0; i < kCPL; ++i) a[i] += v[i];
       }
     }
   }
@@ -697,14 +735,14 @@ struct PipeAcc {
 // k+1 (d_nxt, rk_nxt); stage k is in cur_buf.  Issuing the indices of stage
 // k+3 before the rows of stage k+2 keeps that order, so waiting for idx_cur
 // never waits for the rows of stage k+1 (vmcnt retires in issue order).
-template <typename T, int kSlots>
+template <typename T, int kSlots, int kCPL>
 __device__ __forceinline__ void pipe_step(
     int k, int nst, int64_t s, int64_t e, const char *__restrict__ xb, int64_t ld_bytes,
-    int col_bytes, int rowq, int cb, int rd_c, bool acc_lane, const uint32_t *__restrict__ kw,
+    int col_bytes, int rowq, int cb, bool summer, const uint32_t *__restrict__ kw,
     const uint32_t (&idx_cur)[kSlots], uint32_t (&idx_nxt)[kSlots], u32x4 *__restrict__ cur_buf,
     int *__restrict__ cur_rk, u32x4 (&d_cur)[kSlots], int &rk_cur, u32x4 *__restrict__ nxt_buf,
-    int *__restrict__ nxt_rk, const u32x4 (&d_nxt)[kSlots], const int &rk_nxt, PipeAcc<T> &st,
-    float *__restrict__ out, int64_t row_elems) {
+    int *__restrict__ nxt_rk, const u32x4 (&d_nxt)[kSlots], const int &rk_nxt,
+    PipeAcc<T, kCPL> &st, float *__restrict__ out, int64_t row_elems) {
   auto rows_of = [&](int kk) -> int {
     const int64_t b = s + int64_t(kk) * kStageRows;
     return b >= e ? 0 : int(e - b < kStageRows ? e - b : kStageRows);
@@ -714,9 +752,10 @@ __device__ __forceinline__ void pipe_step(
   // stage k+2: gather its rows and ranks
   stage_load(xb, ld_bytes, col_bytes, rowq, idx_cur, d_cur);
   rk_cur = kw[2 * stage_row_pos(s, e, k + 2) + 1];
-  // stage k: sum it
-  st.add_stage(reinterpret_cast<const typename T::raw *>(cur_buf), cur_rk, rows_of(k), cb, rd_c,
-               acc_lane, out, row_elems);
+  // stage k: sum it (one wave)
+  if (summer)
+    st.add_stage(reinterpret_cast<const typename T::raw *>(cur_buf), cur_rk, rows_of(k), cb,
+                 out, row_elems);
   // stage k+1: into the other LDS buffer (its old contents were summed in step k-1)
   if (k + 1 < nst) {
     stage_store(nxt_buf, rowq, rows_of(k + 1), d_nxt);
@@ -725,7 +764,7 @@ __device__ __forceinline__ void pipe_step(
   __syncthreads();
 }
 
-template <typename T, int kSlots>
+template <typename T, int kSlots, int kCPL>
 __global__ __launch_bounds__(kThreads) void accum_pipe_kernel(
     const char *__restrict__ xb, int64_t ld_bytes, int C, int CB,
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
@@ -755,12 +794,9 @@ __global__ __launch_bounds__(kThreads) void accum_pipe_kernel(
   for (int c0 = 0; c0 < C; c0 += CB) {
     const int cb = C - c0 < CB ? C - c0 : CB;
     const int rowq = cb * int(sizeof(raw)) / 16;
-    const int cpw = (cb + kWaves - 1) / kWaves;
-    const int my_c = w * cpw + lane;
-    const bool acc_lane = lane < cpw && my_c < cb;
-    const int rd_c = acc_lane ? my_c : 0;
+    const bool summer = __builtin_amdgcn_readfirstlane(w) == 0;  // wave-uniform
     const int col_bytes = c0 * int(sizeof(raw));
-    float *out = acc + c0 + my_c;
+    float *out = acc + c0;
 
     uint32_t ia[kSlots], ib[kSlots];
     u32x4 d0[kSlots], d1[kSlots];
@@ -777,14 +813,14 @@ __global__ __launch_bounds__(kThreads) void accum_pipe_kernel(
     if (tid < kStageRows) rk0s[tid] = rk0;
     __syncthreads();
 
-    PipeAcc<T> st;
+    PipeAcc<T, kCPL> st;
     for (int k = 0; k < nst; k += 2) {  // a step past the last stage sums nothing
-      pipe_step<T, kSlots>(k, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, rd_c, acc_lane, kw,
-                           ia, ib, buf0, rk0s, d0, rk0, buf1, rk1s, d1, rk1, st, out, C);
-      pipe_step<T, kSlots>(k + 1, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, rd_c, acc_lane,
-                           kw, ib, ia, buf1, rk1s, d1, rk1, buf0, rk0s, d0, rk0, st, out, C);
+      pipe_step<T, kSlots, kCPL>(k, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, summer, kw,
+                                 ia, ib, buf0, rk0s, d0, rk0, buf1, rk1s, d1, rk1, st, out, C);
+      pipe_step<T, kSlots, kCPL>(k + 1, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, summer,
+                                 kw, ib, ia, buf1, rk1s, d1, rk1, buf0, rk0s, d0, rk0, st, out, C);
     }
-    if (st.cur >= 0 && acc_lane) out[int64_t(st.cur) * C] = st.a;
+    if (summer) st.flush(cb, out, C);
   }
 }
 
@@ -876,22 +912,38 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
 
 // x_grad[p, :] = rows[rank[p], :] (kept) or 0 (dropped); point order, so the
 // writes stream.  V is a 16-byte vector when rows allow it, else one element.
-template <typename V>
+// Each thread copies kPer vectors spaced kThreads apart (coalesced); the
+// destination is written with non-temporal stores (it is not read again
+// here, and keeping it out of L2 leaves room for the gradient rows that are
+// re-read once per point of their cell).  kNarrow: indices fit in 32 bits.
+constexpr int kGatherPer = 4;
+
+template <typename V, bool kNarrow>
 __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const V *__restrict__ rows, int vpr, const int32_t *__restrict__ rank, int64_t n_points,
     V *__restrict__ xg, int64_t xg_ld) {
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  const int64_t p = i / vpr;
-  if (p >= n_points) return;
-  const int q = int(i - p * vpr);
-  const int r = rank[p];
-  V v;
-  if (r >= 0) {
-    v = rows[int64_t(r) * vpr + q];
-  } else {
-    v = V{};
+  const int64_t total = n_points * vpr;
+  const int64_t base = int64_t(blockIdx.x) * (kThreads * kGatherPer) + threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < kGatherPer; ++j) {
+    const int64_t i = base + j * kThreads;
+    if (i < total) {
+      int64_t p;
+      int q;
+      if (kNarrow) {
+        const uint32_t ui = uint32_t(i), up = ui / uint32_t(vpr);
+        p = up;
+        q = int(ui - up * uint32_t(vpr));
+      } else {
+        p = i / vpr;
+        q = int(i - p * vpr);
+      }
+      const int r = rank[p];
+      V v = V{};
+      if (r >= 0) v = rows[int64_t(r) * vpr + q];
+      __builtin_nontemporal_store(v, xg + p * xg_ld + q);
+    }
   }
-  xg[p * xg_ld + q] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -965,14 +1017,14 @@ int check_index_args(int64_t n_points, int64_t n_cells, const void *rank, const 
 
 size_t dtype_size(int32_t dtype) { return dtype == BEVPOOL_F32 ? 4 : 2; }
 
-template <typename T>
+template <typename T, int kCPL>
 int launch_accum_pipe_t(int slots, unsigned grid, size_t smem, hipStream_t s, const char *x,
                         int64_t ld_bytes, int C, int CB, const uint64_t *keys,
                         const int32_t *meta, const int32_t *cend, float *acc) {
 #define BEVPOOL_PIPE_CASE(K)                                                                   \
   case K:                                                                                      \
-    hipLaunchKernelGGL((accum_pipe_kernel<T, K>), dim3(grid), dim3(kThreads), smem, s, x,      \
-                       ld_bytes, C, CB, keys, meta, cend, acc, kRangePoints);                  \
+    hipLaunchKernelGGL((accum_pipe_kernel<T, K, kCPL>), dim3(grid), dim3(kThreads), smem, s,   \
+                       x, ld_bytes, C, CB, keys, meta, cend, acc, kRangePoints);               \
     break;
   switch (slots) {
     BEVPOOL_PIPE_CASE(1)
@@ -990,20 +1042,30 @@ int launch_accum_pipe_t(int slots, unsigned grid, size_t smem, hipStream_t s, co
   return check_launch("accum_pipe");
 }
 
+// Channels per summing lane for a block of CB channels: 1 (<= 64), 2 (<= 128)
+// or 4 (<= 256).
+int pipe_cpl(int CB) { return CB <= 64 ? 1 : (CB <= 128 ? 2 : 4); }
+
 int launch_accum_pipe(int32_t dtype, int slots, unsigned grid, size_t smem, hipStream_t s,
                       const char *x, int64_t ld_bytes, int C, int CB, const uint64_t *keys,
                       const int32_t *meta, const int32_t *cend, float *acc) {
+  const int cpl = pipe_cpl(CB);
+#define BEVPOOL_PIPE_ARGS slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc
   switch (dtype) {
     case BEVPOOL_F32:
-      return launch_accum_pipe_t<F32>(slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend,
-                                      acc);
+      return cpl == 1 ? launch_accum_pipe_t<F32, 1>(BEVPOOL_PIPE_ARGS)
+             : cpl == 2 ? launch_accum_pipe_t<F32, 2>(BEVPOOL_PIPE_ARGS)
+                        : launch_accum_pipe_t<F32, 4>(BEVPOOL_PIPE_ARGS);
     case BEVPOOL_F16:
-      return launch_accum_pipe_t<F16>(slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend,
-                                      acc);
+      return cpl == 1   ? launch_accum_pipe_t<F16, 1>(BEVPOOL_PIPE_ARGS)
+             : cpl == 2 ? launch_accum_pipe_t<F16, 2>(BEVPOOL_PIPE_ARGS)
+                        : launch_accum_pipe_t<F16, 4>(BEVPOOL_PIPE_ARGS);
     default:
-      return launch_accum_pipe_t<BF16>(slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta,
-                                       cend, acc);
+      return cpl == 1   ? launch_accum_pipe_t<BF16, 1>(BEVPOOL_PIPE_ARGS)
+             : cpl == 2 ? launch_accum_pipe_t<BF16, 2>(BEVPOOL_PIPE_ARGS)
+                        : launch_accum_pipe_t<BF16, 4>(BEVPOOL_PIPE_ARGS);
   }
+#undef BEVPOOL_PIPE_ARGS
 }
 
 }  // namespace
@@ -1226,12 +1288,14 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
                        reinterpret_cast<uintptr_t>(feats) % 16 == 0;
     const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
     if (vec16) {
-      // channel block of at most 512 bytes per row: <= 8 16-byte slots per thread per stage
-      const int CBmax = int(512 / es);
+      // channel block of at most 384 bytes per row: <= 6 16-byte slots per thread per
+      // stage and two stages + ranks in <= 48.5 KB of LDS (three blocks per CU)
+      const int CBmax = int(384 / es);
       const int CB = C < CBmax ? C : CBmax;
       const int rowq = int(size_t(CB) * es / 16);
       const int slots = (kStageRows * rowq + kThreads - 1) / kThreads;
       const size_t smem = size_t(2) * kStageRows * rowq * 16 + size_t(2) * kStageRows * sizeof(int);
+      if (smem > 65536) return fail(BEVPOOL_EINVAL, "internal: %zu bytes of LDS", smem);
       LaunchTimer t("accum_rows", s);
       st = launch_accum_pipe(dtype, slots, grid, smem, s, static_cast<const char *>(feats),
                              int64_t(size_t(feats_row_stride) * es), C, CB, keys, meta, cell_end,
@@ -1336,24 +1400,25 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                      (reinterpret_cast<uintptr_t>(x_grad) % 16 == 0) &&
                      (reinterpret_cast<uintptr_t>(scratch) % 16 == 0);
   LaunchTimer t("gather_rows", s);
+  const int vpr = vec16 ? int(row_bytes / 16) : int(C);
+  const int64_t total = n_points * vpr;
+  const unsigned grid = unsigned(ceil_div(total, int64_t(kThreads) * kGatherPer));
+  const bool narrow = total < (int64_t(1) << 32);
+#define BEVPOOL_GATHER(V, NARROW, LD)                                                          \
+  hipLaunchKernelGGL((gather_rows_kernel<V, NARROW>), dim3(grid), dim3(kThreads), 0, s,        \
+                     static_cast<const V *>(scratch), vpr, rank, n_points,                    \
+                     static_cast<V *>(x_grad), LD)
   if (vec16) {
-    const int vpr = int(row_bytes / 16);
     const int64_t ld = int64_t(size_t(x_grad_row_stride) * es / 16);
-    const unsigned grid = unsigned(ceil_div(n_points * vpr, kThreads));
-    hipLaunchKernelGGL(gather_rows_kernel<uint4>, dim3(grid), dim3(kThreads), 0, s,
-                       static_cast<const uint4 *>(scratch), vpr, rank, n_points,
-                       static_cast<uint4 *>(x_grad), ld);
+    if (narrow) BEVPOOL_GATHER(u32x4, true, ld); else BEVPOOL_GATHER(u32x4, false, ld);
   } else if (es == 4) {
-    const unsigned grid = unsigned(ceil_div(n_points * C, kThreads));
-    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3(grid), dim3(kThreads), 0, s,
-                       static_cast<const uint32_t *>(scratch), int(C), rank, n_points,
-                       static_cast<uint32_t *>(x_grad), x_grad_row_stride);
+    if (narrow) BEVPOOL_GATHER(uint32_t, true, x_grad_row_stride);
+    else BEVPOOL_GATHER(uint32_t, false, x_grad_row_stride);
   } else {
-    const unsigned grid = unsigned(ceil_div(n_points * C, kThreads));
-    hipLaunchKernelGGL(gather_rows_kernel<uint16_t>, dim3(grid), dim3(kThreads), 0, s,
-                       static_cast<const uint16_t *>(scratch), int(C), rank, n_points,
-                       static_cast<uint16_t *>(x_grad), x_grad_row_stride);
+    if (narrow) BEVPOOL_GATHER(uint16_t, true, x_grad_row_stride);
+    else BEVPOOL_GATHER(uint16_t, false, x_grad_row_stride);
   }
+#undef BEVPOOL_GATHER
   return check_launch("gather_rows");
 }
 
