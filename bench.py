@@ -99,6 +99,9 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--profile-steps', type=int, default=10,
                     help='steps run with per-kernel HIP-event timing')
+    ap.add_argument('--mode', default='bench', choices=['bench', 'kernels'],
+                    help="'kernels': run --steps plain fwd+bwd steps and a 512 MiB device copy "
+                         '(the traffic calibrator for rocprofv3 --pmc passes), print nothing')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}): the bev_pool path '
@@ -141,6 +144,18 @@ def main():
         step()
     torch.cuda.synchronize()
 
+    if args.mode == 'kernels':
+        for _ in range(args.steps):
+            step()
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        for _ in range(3):
+            dst.copy_(src)  # plain copy: 512 MiB read + 512 MiB written per launch
+        torch.cuda.synchronize()
+        log('[bench] kernels mode done')
+        return
+
     log(f'[bench] timing {args.steps} steps')
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -155,8 +170,9 @@ def main():
     gpu_ms = ev0.elapsed_time(ev1)
     ms_per_step = wall_s * 1e3 / args.steps
 
-    # forward / backward split (HIP events around each half, median)
-    fwd_ms, bwd_ms = [], []
+    # forward / backward split: HIP events around each half of 20 back-to-back
+    # steps (one synchronisation at the end, so launch latency stays hidden)
+    evs = []
     for _ in range(20):
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         e[0].record()
@@ -164,11 +180,10 @@ def main():
         e[1].record()
         torch.autograd.grad(out, x, g)
         e[2].record()
-        torch.cuda.synchronize()
-        fwd_ms.append(e[0].elapsed_time(e[1]))
-        bwd_ms.append(e[1].elapsed_time(e[2]))
-    t_fwd = statistics.median(fwd_ms)
-    t_bwd = statistics.median(bwd_ms)
+        evs.append(e)
+    torch.cuda.synchronize()
+    t_fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+    t_bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
 
     # per-kernel durations from HIP events on the launch stream
     log(f'[bench] per-kernel timing over {args.profile_steps} steps')
@@ -190,6 +205,26 @@ def main():
         if b is not None and k['avg_us'] > 0:
             k['alg_GBps'] = round(b / (k['avg_us'] * 1e-6) / 1e9, 1)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9 if dom_bytes else None
+
+    # bandwidth calibration: a plain fill and a plain copy of the feature
+    # tensor's byte count (torch kernels), HIP-event timed
+    cal_bytes = x.numel() * x.element_size()
+    buf_a = torch.empty(cal_bytes, dtype=torch.uint8, device=dev)
+    buf_b = torch.empty_like(buf_a)
+    buf_a.fill_(0)
+    buf_b.copy_(buf_a)
+    cal = {}
+    for name, fn, moved in (('fill', lambda: buf_a.fill_(1), cal_bytes),
+                            ('copy', lambda: buf_b.copy_(buf_a), 2 * cal_bytes)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        cal[f'{name}_GBps'] = round(moved * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    cal['bytes'] = cal_bytes
+    del buf_a, buf_b
 
     traffic = None
     tfile = ROOT / 'profiles' / f'traffic_{args.config}.json'
@@ -233,6 +268,7 @@ def main():
             'avg_us': dom_us,
         },
         'kernels': kernels,
+        'calibration': cal,
     }
 
     if not args.no_cpu_baseline:

@@ -59,7 +59,10 @@ constexpr int kWaveItems = 64 * kItems;    // 1024 keys per wave in the scatter
 constexpr int kMaxDigitBits = 10;
 constexpr int kMaxRadix = 1 << kMaxDigitBits;
 constexpr int kCellTile = 64;              // cells per transpose tile
-constexpr int64_t kRangePoints = 512;      // nominal sorted points per forward range
+#ifndef BEVPOOL_RANGE_POINTS
+#define BEVPOOL_RANGE_POINTS 512
+#endif
+constexpr int64_t kRangePoints = BEVPOOL_RANGE_POINTS;  // nominal sorted points per forward range
 
 // ---------------------------------------------------------------------------
 // error reporting
@@ -589,183 +592,238 @@ __global__ __launch_bounds__(kThreads) void accum_rows_kernel(
 // ---- software-pipelined forward accumulation (16-byte rows) ---------------
 //
 // Same ownership as accum_rows_kernel (block b owns the sorted positions
-// [snap(b*P), snap((b+1)*P)), whole cells only), restructured so that memory
-// latency is hidden inside the block:
-//   * the range is cut into stages of kStageRows sorted points; a stage's
-//     rows are gathered with 16-byte loads (slot i of thread t covers row
-//     (t + 256 i) / rowq, 16-byte column (t + 256 i) % rowq) into registers;
-//   * two stages are in flight while a third is accumulated from LDS: loads
-//     of stage k+2 and the point indices of stage k+3 are issued before stage
-//     k is summed, stage k+1 is written to LDS after it; one barrier a stage;
-//   * the channels are spread over the four waves (wave w, lane l owns channel
-//     w*ceil(C/4) + l), each lane adding its column of the stage in order into
-//     one fp32 accumulator; a cell's sum is stored to acc when the next cell
-//     starts (start flags from a ballot over the stage's ranks) or the range
-//     ends, so a cell spanning stages keeps one sequential chain.
-constexpr int kStageRows = 64;
+// [snap(b*P), snap((b+1)*P)), whole cells only), restructured so memory
+// latency is hidden inside the block.  Roles:
+//   * loader waves (1..4, 256 threads) gather the rows of each stage of
+//     kStageRows sorted points with 16-byte loads (loader slot i of thread t
+//     covers row (t + 256 i) / rowq, 16-byte column (t + 256 i) % rowq) into
+//     a ring of kDepth register stages, and move the oldest arrived stage to
+//     LDS once per step;
+//   * wave 0 sums the stage in LDS, one channel per lane (channels l + 64 j),
+//     each lane adding its column in row order into one fp32 accumulator; a
+//     cell's sum is stored to acc when the next cell starts (start flags from
+//     a ballot over the stage's ranks) or the range ends, so a cell spanning
+//     stages keeps one sequential chain.
+// Step k: wave 0 sums stage k from LDS buffer k&1 while the loaders issue the
+// rows of stage k+kDepth and the point indices of stage k+2*kDepth, then store
+// stage k+1 (issued kDepth-1 steps earlier) into buffer (k+1)&1; one barrier.
+// The loaders issue loads only and always fetch a stage's indices kDepth steps
+// before its rows, so every wait they need (indices of stage k+kDepth, rows of
+// stage k+1) leaves all younger row loads in flight (vmcnt retires in issue
+// order).  The summing wave issues no loads, so its stores never hold up a
+// wait.  Loads of stages past the range end are pointed at the range's first
+// row (a single line) so the code stays straight-line.
+#ifndef BEVPOOL_STAGE_ROWS
+#define BEVPOOL_STAGE_ROWS 32
+#endif
+#ifndef BEVPOOL_DEPTH
+#define BEVPOOL_DEPTH 2
+#endif
+constexpr int kStageRows = BEVPOOL_STAGE_ROWS;  // sorted points per stage (power of 2, <= 64)
+constexpr int kDepth = BEVPOOL_DEPTH;           // row stages in flight per loader thread
+#ifndef BEVPOOL_SUMMERS
+#define BEVPOOL_SUMMERS 1
+#endif
+#ifndef BEVPOOL_LOADER_WAVES
+#define BEVPOOL_LOADER_WAVES 2
+#endif
+constexpr int kSummers = BEVPOOL_SUMMERS;       // summing waves (waves 0..kSummers-1)
+constexpr int kLoaders = 64 * BEVPOOL_LOADER_WAVES;  // loader threads (the other waves)
+constexpr int kPipeThreads = 64 * kSummers + kLoaders;
+static_assert(kStageRows <= 64 && (kStageRows & (kStageRows - 1)) == 0, "stage rows");
 
-// native 16-byte vector (register-promotable, unlike the HIP u32x4 wrapper)
+// native 16-byte vector (register-promotable, unlike the HIP uint4 wrapper)
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// Point indices of one stage.  Every slot is loaded (straight-line code keeps
-// the compiler's vmcnt accounting exact): slots past the stage's rows repeat
-// its last row, and a stage past the range end reads the range's first row.
+struct PipeRange {
+  int64_t s, e;  // sorted positions [s, e)
+  int rowq;      // 16-byte slots per row of this channel block
+  __device__ __forceinline__ int rows(int k) const {
+    const int64_t b = s + int64_t(k) * kStageRows;
+    return b >= e ? 0 : int(e - b < kStageRows ? e - b : kStageRows);
+  }
+};
+
+// Register ring of one loader thread.
 template <int kSlots>
-__device__ __forceinline__ void stage_index(const uint32_t *__restrict__ kw, int64_t base,
-                                            int rowq, int rows, int64_t first,
-                                            uint32_t (&idx)[kSlots]) {
+struct LoaderRing {
+  u32x4 d[kDepth][kSlots];       // gathered 16-byte pieces of a stage
+  uint32_t idx[kDepth][kSlots];  // point indices of a later stage
+  int rk[kDepth];                // rank of row (lt % kStageRows) of a stage
+};
+
+// Point indices of stage k into ring slot j.  Slots past the stage's rows
+// repeat its last row; a stage past the range end reads the range's first row.
+template <int kSlots, int j>
+__device__ __forceinline__ void ring_index(LoaderRing<kSlots> &R, int lt,
+                                           const uint32_t *__restrict__ kw, const PipeRange &pr,
+                                           int k) {
+  const int rows = pr.rows(k);
+  const int64_t base = pr.s + int64_t(k) * kStageRows;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    const int slot = int(threadIdx.x) + kThreads * i;
-    int r = slot / rowq;
+    int r = (lt + kLoaders * i) / pr.rowq;
     r = r < rows - 1 ? r : rows - 1;
-    idx[i] = kw[2 * (rows > 0 ? base + r : first)];  // low word: point index
+    R.idx[j][i] = kw[2 * (rows > 0 ? base + r : pr.s)];  // low word: point index
   }
 }
 
-template <int kSlots>
-__device__ __forceinline__ void stage_load(const char *__restrict__ xb, int64_t ld_bytes,
-                                           int col_bytes, int rowq,
-                                           const uint32_t (&idx)[kSlots], u32x4 (&d)[kSlots]) {
+// Rows of stage k into ring slot j (its indices are in R.idx[j]), plus the rank
+// of row lt % kStageRows.
+template <int kSlots, int j>
+__device__ __forceinline__ void ring_rows(LoaderRing<kSlots> &R, int lt,
+                                          const uint32_t *__restrict__ kw,
+                                          const char *__restrict__ xb, int64_t ld_bytes,
+                                          int col_bytes, const PipeRange &pr, int k) {
+  const bool live = pr.rows(k) > 0;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    const int slot = int(threadIdx.x) + kThreads * i;
-    const int q = slot - (slot / rowq) * rowq;
-    d[i] = *reinterpret_cast<const u32x4 *>(xb + int64_t(idx[i]) * ld_bytes + col_bytes +
-                                             q * 16);
+    const int slot = lt + kLoaders * i;
+    const int q = live ? slot - (slot / pr.rowq) * pr.rowq : 0;
+    R.d[j][i] = *reinterpret_cast<const u32x4 *>(xb + int64_t(R.idx[j][i]) * ld_bytes +
+                                                 col_bytes + q * 16);
   }
+  const int64_t b = pr.s + int64_t(k) * kStageRows;
+  int64_t p = b + (lt & (kStageRows - 1));
+  p = b >= pr.e ? pr.s : (p < pr.e ? p : pr.e - 1);
+  R.rk[j] = kw[2 * p + 1];  // high word: rank
 }
 
-// Sorted position whose rank thread t (< kStageRows) stages for stage k:
-// row t of the stage, clamped into the range like stage_index.
-__device__ __forceinline__ int64_t stage_row_pos(int64_t s, int64_t e, int k) {
-  const int64_t b = s + int64_t(k) * kStageRows;
-  if (b >= e) return s;
-  const int64_t p = b + (threadIdx.x & (kStageRows - 1));
-  return p < e ? p : e - 1;
-}
-
-template <int kSlots>
-__device__ __forceinline__ void stage_store(u32x4 *__restrict__ lbuf, int rowq, int rows,
-                                            const u32x4 (&d)[kSlots]) {
+// Ring slot j (stage k) into an LDS buffer.
+template <int kSlots, int j>
+__device__ __forceinline__ void ring_store(const LoaderRing<kSlots> &R, int lt,
+                                           const PipeRange &pr, int k, u32x4 *__restrict__ lbuf,
+                                           int *__restrict__ lrk) {
+  const int n = pr.rows(k) * pr.rowq;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    const int slot = int(threadIdx.x) + kThreads * i;
-    if (slot < rows * rowq) lbuf[slot] = d[i];
+    const int slot = lt + kLoaders * i;
+    if (slot < n) lbuf[slot] = R.d[j][i];
   }
+  if (lt < kStageRows) lrk[lt] = R.rk[j];
 }
 
-// Channels l, l+64, ... of one LDS row (lane l), widened to fp32.  Columns
-// past the block are clamped to its last channel (read, never stored).  Each
-// channel is a separate 32/16-bit read and a separate scalar add: no 2-wide
-// float vector is ever formed (with packed fp32 ops disabled, hipcc 7.2
-// lowers a <2 x float> add of a 64-bit LDS load to two adds of its low half).
-template <typename T, int kCPL>
-__device__ __forceinline__ void load_channels(const typename T::raw *__restrict__ row,
-                                              const int (&col)[kCPL], float (&v)[kCPL]) {
-#pragma unroll
-  for (int i = 0; i < kCPL; ++i) v[i] = T::load(row + col[i]);
+// One loader step k with ring slot r = k % kDepth (a template constant).
+template <int kSlots, int r>
+__device__ __forceinline__ void loader_step(LoaderRing<kSlots> &R, int lt,
+                                            const uint32_t *__restrict__ kw,
+                                            const char *__restrict__ xb, int64_t ld_bytes,
+                                            int col_bytes, const PipeRange &pr, int k, int nst,
+                                            u32x4 *__restrict__ buf0, u32x4 *__restrict__ buf1,
+                                            int *__restrict__ rk0s, int *__restrict__ rk1s) {
+  ring_rows<kSlots, r>(R, lt, kw, xb, ld_bytes, col_bytes, pr, k + kDepth);
+  ring_index<kSlots, r>(R, lt, kw, pr, k + 2 * kDepth);
+  if (k + 1 < nst) {
+    if ((k + 1) & 1)
+      ring_store<kSlots, (r + 1) % kDepth>(R, lt, pr, k + 1, buf1, rk1s);
+    else
+      ring_store<kSlots, (r + 1) % kDepth>(R, lt, pr, k + 1, buf0, rk0s);
+  }
+  __syncthreads();
 }
 
-// Per-lane running sums of one wave that owns all the channels of a block:
-// lane l holds channels l + 64 i, i < kCPL.  The stage's rows are walked cell
-// segment by cell segment: the next start bit is found with ctz, the rows of
-// the segment are added in order in a tight loop, and the finished cell is
-// stored when the next one starts.
+// Sequential per-channel sums of one stage by one summing wave: lane l owns
+// channels c0 + l + 64 i (i < kCPL, c0 the wave's first channel).  Rows are
+// read from LDS 16 at a time before they are added (one LDS latency per 16
+// dependent adds).  A 16-row chunk without a cell start is 16 straight adds;
+// a chunk with exactly one start at row b jumps (16-way switch) to
+// straight-line code for that b: add rows [0, b), store the finished cell,
+// restart from +0.0, add rows [b, 16); other chunks go row by row.
 template <typename T, int kCPL>
-struct PipeAcc {
+struct RowSum {
   float a[kCPL];
   int cur = -1;    // rank of the current cell
   int carry = -1;  // rank of the previous stage's last row
 
-  __device__ __forceinline__ void flush(int cb, float *__restrict__ out, int64_t row_elems) {
+  __device__ __forceinline__ void flush(int nch, float *__restrict__ out, int64_t row_elems) {
     if (cur >= 0) {
       float *o = out + int64_t(cur) * row_elems;
       const int lane = lane_id();
 #pragma unroll
       for (int i = 0; i < kCPL; ++i)
-        if (lane + 64 * i < cb) o[lane + 64 * i] = a[i];
+        if (lane + 64 * i < nch) o[lane + 64 * i] = a[i];
     }
   }
 
+  template <int kB, int kStart>
+  __device__ __forceinline__ void split_chunk(const float (&v)[kB][kCPL], int rkl, int j0, int nch,
+                                              float *__restrict__ out, int64_t row_elems) {
+#pragma unroll
+    for (int u = 0; u < kStart; ++u)
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+    flush(nch, out, row_elems);
+#pragma unroll
+    for (int i = 0; i < kCPL; ++i) a[i] = 0.0f;
+    cur = __builtin_amdgcn_readlane(rkl, j0 + kStart);
+#pragma unroll
+    for (int u = kStart; u < kB; ++u)
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+  }
+
+  // lb: the stage's rows in LDS (row stride cb elements), col: this lane's
+  // columns; nch: channels of this wave (stores of lanes past nch are skipped).
   __device__ __forceinline__ void add_stage(const typename T::raw *__restrict__ lb,
                                             const int *__restrict__ lrk, int rows, int cb,
+                                            const int (&col)[kCPL], int nch,
                                             float *__restrict__ out, int64_t row_elems) {
     const int lane = lane_id();
-    int col[kCPL];
-#pragma unroll
-    for (int i = 0; i < kCPL; ++i) col[i] = lane + 64 * i < cb ? lane + 64 * i : cb - 1;
     const int rkl = lane < rows ? lrk[lane] : -1;
     int prev = __shfl_up(rkl, 1, 64);
     if (lane == 0) prev = carry;
     const uint64_t starts = __ballot(lane < rows && rkl != prev);
     if (rows > 0) carry = __builtin_amdgcn_readlane(rkl, rows - 1);
-    int j = 0;
-    while (j < rows) {
-      if ((starts >> j) & 1) {
-        flush(cb, out, row_elems);
+    constexpr int kB = kStageRows < 16 ? kStageRows : 16;
+    for (int j0 = 0; j0 < rows; j0 += kB) {
+      float v[kB][kCPL];
 #pragma unroll
-        for (int i = 0; i < kCPL; ++i) a[i] = 0.0f;
-        cur = __builtin_amdgcn_readlane(rkl, j);
-      }
-      const uint64_t later = j + 1 < 64 ? (starts >> (j + 1)) : 0;
-      int next = later ? j + 1 + int(__builtin_ctzll(later)) : rows;
-      next = next < rows ? next : rows;
-      for (; j + 4 <= next; j += 4) {
-        float v[4][kCPL];
+      for (int u = 0; u < kB; ++u)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) load_channels<T, kCPL>(lb + (j + u) * cb, col, v[u]);
+        for (int i = 0; i < kCPL; ++i) v[u][i] = T::load(lb + (j0 + u) * cb + col[i]);
+      const uint32_t chunk = uint32_t(starts >> j0) & uint32_t((uint64_t(1) << kB) - 1);
+      const bool full = j0 + kB <= rows;
+      if (full && chunk == 0) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < kB; ++u)
 #pragma unroll
           for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
-      }
-      for (; j < next; ++j) {
-        float v[kCPL];
-        load_channels<T, kCPL>(lb + j * cb, col, v);
+      } else if (full && (chunk & (chunk - 1)) == 0) {
+        switch (__builtin_ctz(chunk)) {
+#define BEVPOOL_SPLIT(B)                                                                       \
+  case B:                                                                                     \
+    if constexpr ((B) < kB) split_chunk<kB, ((B) < kB ? (B) : 0)>(v, rkl, j0, nch, out, row_elems); \
+    break;
+          BEVPOOL_SPLIT(0) BEVPOOL_SPLIT(1) BEVPOOL_SPLIT(2) BEVPOOL_SPLIT(3)
+          BEVPOOL_SPLIT(4) BEVPOOL_SPLIT(5) BEVPOOL_SPLIT(6) BEVPOOL_SPLIT(7)
+          BEVPOOL_SPLIT(8) BEVPOOL_SPLIT(9) BEVPOOL_SPLIT(10) BEVPOOL_SPLIT(11)
+          BEVPOOL_SPLIT(12) BEVPOOL_SPLIT(13) BEVPOOL_SPLIT(14) BEVPOOL_SPLIT(15)
+#undef BEVPOOL_SPLIT
+          default:
+            break;
+        }
+      } else {
 #pragma unroll
-        for (int i = 0; i < kCPL; ++i) a[i] += v[i];
+        for (int u = 0; u < kB; ++u) {
+          const int j = j0 + u;
+          if (j < rows) {
+            if ((chunk >> u) & 1) {
+              flush(nch, out, row_elems);
+#pragma unroll
+              for (int i = 0; i < kCPL; ++i) a[i] = 0.0f;
+              cur = __builtin_amdgcn_readlane(rkl, j);
+            }
+#pragma unroll
+            for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+          }
+        }
       }
     }
   }
 };
 
-// One pipeline step.  On entry the loads still in flight are, in issue order,
-// the point indices of stage k+2 (idx_cur), then the rows and ranks of stage
-// k+1 (d_nxt, rk_nxt); stage k is in cur_buf.  Issuing the indices of stage
-// k+3 before the rows of stage k+2 keeps that order, so waiting for idx_cur
-// never waits for the rows of stage k+1 (vmcnt retires in issue order).
 template <typename T, int kSlots, int kCPL>
-__device__ __forceinline__ void pipe_step(
-    int k, int nst, int64_t s, int64_t e, const char *__restrict__ xb, int64_t ld_bytes,
-    int col_bytes, int rowq, int cb, bool summer, const uint32_t *__restrict__ kw,
-    const uint32_t (&idx_cur)[kSlots], uint32_t (&idx_nxt)[kSlots], u32x4 *__restrict__ cur_buf,
-    int *__restrict__ cur_rk, u32x4 (&d_cur)[kSlots], int &rk_cur, u32x4 *__restrict__ nxt_buf,
-    int *__restrict__ nxt_rk, const u32x4 (&d_nxt)[kSlots], const int &rk_nxt,
-    PipeAcc<T, kCPL> &st, float *__restrict__ out, int64_t row_elems) {
-  auto rows_of = [&](int kk) -> int {
-    const int64_t b = s + int64_t(kk) * kStageRows;
-    return b >= e ? 0 : int(e - b < kStageRows ? e - b : kStageRows);
-  };
-  // stage k+3: its point indices
-  stage_index(kw, s + int64_t(k + 3) * kStageRows, rowq, rows_of(k + 3), s, idx_nxt);
-  // stage k+2: gather its rows and ranks
-  stage_load(xb, ld_bytes, col_bytes, rowq, idx_cur, d_cur);
-  rk_cur = kw[2 * stage_row_pos(s, e, k + 2) + 1];
-  // stage k: sum it (one wave)
-  if (summer)
-    st.add_stage(reinterpret_cast<const typename T::raw *>(cur_buf), cur_rk, rows_of(k), cb,
-                 out, row_elems);
-  // stage k+1: into the other LDS buffer (its old contents were summed in step k-1)
-  if (k + 1 < nst) {
-    stage_store(nxt_buf, rowq, rows_of(k + 1), d_nxt);
-    if (threadIdx.x < kStageRows) nxt_rk[threadIdx.x] = rk_nxt;
-  }
-  __syncthreads();
-}
-
-template <typename T, int kSlots, int kCPL>
-__global__ __launch_bounds__(kThreads) void accum_pipe_kernel(
+__global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
     const char *__restrict__ xb, int64_t ld_bytes, int C, int CB,
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
     const int32_t *__restrict__ cend, float *__restrict__ acc, int64_t P) {
@@ -781,46 +839,73 @@ __global__ __launch_bounds__(kThreads) void accum_pipe_kernel(
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
   const int64_t r0 = int64_t(blockIdx.x) * P;
   if (r0 >= n) return;
-  const int64_t s = snap_to_cell(r0, n, keys, cend);
-  const int64_t e = snap_to_cell(r0 + P < n ? r0 + P : n, n, keys, cend);
-  if (s >= e) return;
-  const int nst = int((e - s + kStageRows - 1) / kStageRows);
-  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
-  auto rows_of = [&](int kk) -> int {
-    const int64_t b = s + int64_t(kk) * kStageRows;
-    return b >= e ? 0 : int(e - b < kStageRows ? e - b : kStageRows);
-  };
+  PipeRange pr;
+  pr.s = snap_to_cell(r0, n, keys, cend);
+  pr.e = snap_to_cell(r0 + P < n ? r0 + P : n, n, keys, cend);
+  if (pr.s >= pr.e) return;
+  const int nst = int((pr.e - pr.s + kStageRows - 1) / kStageRows);
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const bool summer = wave < kSummers;
+  const int lt = int(threadIdx.x) - 64 * kSummers;  // loader thread index (loader waves only)
 
   for (int c0 = 0; c0 < C; c0 += CB) {
     const int cb = C - c0 < CB ? C - c0 : CB;
-    const int rowq = cb * int(sizeof(raw)) / 16;
-    const bool summer = __builtin_amdgcn_readfirstlane(w) == 0;  // wave-uniform
-    const int col_bytes = c0 * int(sizeof(raw));
-    float *out = acc + c0;
-
-    uint32_t ia[kSlots], ib[kSlots];
-    u32x4 d0[kSlots], d1[kSlots];
-    int rk0 = -1, rk1 = -1;
-    // prologue: leave in flight, in order, indices(2) then rows(1); stage 0 in LDS
-    stage_index(kw, s, rowq, rows_of(0), s, ia);
-    stage_index(kw, s + kStageRows, rowq, rows_of(1), s, ib);
-    stage_load(xb, ld_bytes, col_bytes, rowq, ia, d0);
-    rk0 = kw[2 * stage_row_pos(s, e, 0) + 1];
-    stage_index(kw, s + 2 * kStageRows, rowq, rows_of(2), s, ia);
-    stage_load(xb, ld_bytes, col_bytes, rowq, ib, d1);
-    rk1 = kw[2 * stage_row_pos(s, e, 1) + 1];
-    stage_store(buf0, rowq, rows_of(0), d0);
-    if (tid < kStageRows) rk0s[tid] = rk0;
-    __syncthreads();
-
-    PipeAcc<T, kCPL> st;
-    for (int k = 0; k < nst; k += 2) {  // a step past the last stage sums nothing
-      pipe_step<T, kSlots, kCPL>(k, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, summer, kw,
-                                 ia, ib, buf0, rk0s, d0, rk0, buf1, rk1s, d1, rk1, st, out, C);
-      pipe_step<T, kSlots, kCPL>(k + 1, nst, s, e, xb, ld_bytes, col_bytes, rowq, cb, summer,
-                                 kw, ib, ia, buf1, rk1s, d1, rk1, buf0, rk0s, d0, rk0, st, out, C);
+    pr.rowq = cb * int(sizeof(raw)) / 16;
+    if (summer) {
+      // summing wave `wave` owns channels [wch, wch + nch) of the block
+      const int cps = (cb + kSummers - 1) / kSummers;
+      const int wch = wave * cps;
+      const int nch = cb - wch < cps ? (cb - wch > 0 ? cb - wch : 0) : cps;
+      int col[kCPL];
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i) {
+        const int c = lane_id() + 64 * i;
+        const int cc = wch + (c < nch ? c : (nch > 0 ? nch - 1 : 0));
+        col[i] = cc < cb ? cc : cb - 1;  // idle lanes read a valid column
+      }
+      float *out = acc + c0 + wch;
+      RowSum<T, kCPL> st;
+      __syncthreads();  // stage 0 is in buffer 0
+      for (int k = 0; k < nst; k += kDepth) {  // barriers match the loaders'
+#pragma unroll
+        for (int r = 0; r < kDepth; ++r) {
+          const int kk = k + r;
+          st.add_stage(reinterpret_cast<const raw *>((kk & 1) ? buf1 : buf0),
+                       (kk & 1) ? rk1s : rk0s, pr.rows(kk), cb, col, nch, out, C);
+          __syncthreads();
+        }
+      }
+      st.flush(nch, out, C);
+    } else {
+      const int col_bytes = c0 * int(sizeof(raw));
+      LoaderRing<kSlots> R;
+      // prologue: indices of stages 0..D-1, rows of 0..D-1 each followed by the
+      // indices of stage j+D; then stage 0 into LDS
+#define BEVPOOL_RING_PRO(J)                                                                    \
+  if constexpr ((J) < kDepth) ring_index<kSlots, (J)>(R, lt, kw, pr, (J));
+      BEVPOOL_RING_PRO(0) BEVPOOL_RING_PRO(1) BEVPOOL_RING_PRO(2) BEVPOOL_RING_PRO(3)
+      BEVPOOL_RING_PRO(4) BEVPOOL_RING_PRO(5) BEVPOOL_RING_PRO(6) BEVPOOL_RING_PRO(7)
+#undef BEVPOOL_RING_PRO
+#define BEVPOOL_RING_PRO(J)                                                                    \
+  if constexpr ((J) < kDepth) {                                                               \
+    ring_rows<kSlots, (J)>(R, lt, kw, xb, ld_bytes, col_bytes, pr, (J));                      \
+    ring_index<kSlots, (J)>(R, lt, kw, pr, (J) + kDepth);                                     \
+  }
+      BEVPOOL_RING_PRO(0) BEVPOOL_RING_PRO(1) BEVPOOL_RING_PRO(2) BEVPOOL_RING_PRO(3)
+      BEVPOOL_RING_PRO(4) BEVPOOL_RING_PRO(5) BEVPOOL_RING_PRO(6) BEVPOOL_RING_PRO(7)
+#undef BEVPOOL_RING_PRO
+      ring_store<kSlots, 0>(R, lt, pr, 0, buf0, rk0s);
+      __syncthreads();
+      for (int k = 0; k < nst; k += kDepth) {
+#define BEVPOOL_RING_STEP(J)                                                                   \
+  if constexpr ((J) < kDepth)                                                                 \
+    loader_step<kSlots, (J)>(R, lt, kw, xb, ld_bytes, col_bytes, pr, k + (J), nst, buf0, buf1, \
+                             rk0s, rk1s);
+        BEVPOOL_RING_STEP(0) BEVPOOL_RING_STEP(1) BEVPOOL_RING_STEP(2) BEVPOOL_RING_STEP(3)
+        BEVPOOL_RING_STEP(4) BEVPOOL_RING_STEP(5) BEVPOOL_RING_STEP(6) BEVPOOL_RING_STEP(7)
+#undef BEVPOOL_RING_STEP
+      }
     }
-    if (summer) st.flush(cb, out, C);
   }
 }
 
@@ -916,7 +1001,10 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
 // destination is written with non-temporal stores (it is not read again
 // here, and keeping it out of L2 leaves room for the gradient rows that are
 // re-read once per point of their cell).  kNarrow: indices fit in 32 bits.
-constexpr int kGatherPer = 4;
+#ifndef BEVPOOL_GATHER_PER
+#define BEVPOOL_GATHER_PER 4
+#endif
+constexpr int kGatherPer = BEVPOOL_GATHER_PER;
 
 template <typename V, bool kNarrow>
 __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
@@ -1023,8 +1111,8 @@ int launch_accum_pipe_t(int slots, unsigned grid, size_t smem, hipStream_t s, co
                         const int32_t *meta, const int32_t *cend, float *acc) {
 #define BEVPOOL_PIPE_CASE(K)                                                                   \
   case K:                                                                                      \
-    hipLaunchKernelGGL((accum_pipe_kernel<T, K, kCPL>), dim3(grid), dim3(kThreads), smem, s,   \
-                       x, ld_bytes, C, CB, keys, meta, cend, acc, kRangePoints);               \
+    hipLaunchKernelGGL((accum_pipe_kernel<T, K, kCPL>), dim3(grid), dim3(kPipeThreads), smem,  \
+                       s, x, ld_bytes, C, CB, keys, meta, cend, acc, kRangePoints);            \
     break;
   switch (slots) {
     BEVPOOL_PIPE_CASE(1)
@@ -1042,29 +1130,31 @@ int launch_accum_pipe_t(int slots, unsigned grid, size_t smem, hipStream_t s, co
   return check_launch("accum_pipe");
 }
 
-// Channels per summing lane for a block of CB channels: 1 (<= 64), 2 (<= 128)
-// or 4 (<= 256).
-int pipe_cpl(int CB) { return CB <= 64 ? 1 : (CB <= 128 ? 2 : 4); }
+// Channels per summing lane for a block of CB channels split over kSummers
+// waves: 1 (<= 64 per wave), 2 (<= 128) or 4 (<= 256).
+int pipe_cpl(int CB) {
+  const int cps = (CB + kSummers - 1) / kSummers;
+  return cps <= 64 ? 1 : (cps <= 128 ? 2 : 4);
+}
 
 int launch_accum_pipe(int32_t dtype, int slots, unsigned grid, size_t smem, hipStream_t s,
                       const char *x, int64_t ld_bytes, int C, int CB, const uint64_t *keys,
                       const int32_t *meta, const int32_t *cend, float *acc) {
   const int cpl = pipe_cpl(CB);
 #define BEVPOOL_PIPE_ARGS slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc
+#define BEVPOOL_PIPE_DTYPE(T)                                                                  \
+  return cpl == 1   ? launch_accum_pipe_t<T, 1>(BEVPOOL_PIPE_ARGS)                            \
+         : cpl == 2 ? launch_accum_pipe_t<T, 2>(BEVPOOL_PIPE_ARGS)                            \
+                    : launch_accum_pipe_t<T, 4>(BEVPOOL_PIPE_ARGS);
   switch (dtype) {
     case BEVPOOL_F32:
-      return cpl == 1 ? launch_accum_pipe_t<F32, 1>(BEVPOOL_PIPE_ARGS)
-             : cpl == 2 ? launch_accum_pipe_t<F32, 2>(BEVPOOL_PIPE_ARGS)
-                        : launch_accum_pipe_t<F32, 4>(BEVPOOL_PIPE_ARGS);
+      BEVPOOL_PIPE_DTYPE(F32)
     case BEVPOOL_F16:
-      return cpl == 1   ? launch_accum_pipe_t<F16, 1>(BEVPOOL_PIPE_ARGS)
-             : cpl == 2 ? launch_accum_pipe_t<F16, 2>(BEVPOOL_PIPE_ARGS)
-                        : launch_accum_pipe_t<F16, 4>(BEVPOOL_PIPE_ARGS);
+      BEVPOOL_PIPE_DTYPE(F16)
     default:
-      return cpl == 1   ? launch_accum_pipe_t<BF16, 1>(BEVPOOL_PIPE_ARGS)
-             : cpl == 2 ? launch_accum_pipe_t<BF16, 2>(BEVPOOL_PIPE_ARGS)
-                        : launch_accum_pipe_t<BF16, 4>(BEVPOOL_PIPE_ARGS);
+      BEVPOOL_PIPE_DTYPE(BF16)
   }
+#undef BEVPOOL_PIPE_DTYPE
 #undef BEVPOOL_PIPE_ARGS
 }
 
@@ -1293,7 +1383,7 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
       const int CBmax = int(384 / es);
       const int CB = C < CBmax ? C : CBmax;
       const int rowq = int(size_t(CB) * es / 16);
-      const int slots = (kStageRows * rowq + kThreads - 1) / kThreads;
+      const int slots = (kStageRows * rowq + kLoaders - 1) / kLoaders;
       const size_t smem = size_t(2) * kStageRows * rowq * 16 + size_t(2) * kStageRows * sizeof(int);
       if (smem > 65536) return fail(BEVPOOL_EINVAL, "internal: %zu bytes of LDS", smem);
       LaunchTimer t("accum_rows", s);
