@@ -81,6 +81,67 @@ def kernel_alg_bytes(name, n_all, n_kept, n_occ, cells, C, s=4):
     return table.get(name)
 
 
+KERNEL_TIMER_NAMES = (
+    # device kernel -> name the library's launch timer uses
+    ('accum_pipe_kernel', 'accum_rows'), ('accum_rows_kernel', 'accum_rows'),
+    ('gather_rows_kernel', 'gather_rows'), ('rows_to_bev_kernel', 'rows_to_bev'),
+    ('bev_to_rows_kernel', 'bev_to_rows'), ('quantize_geom_kernel', 'quantize_geom'),
+    ('coord_ranks_kernel', 'coord_ranks'), ('radix_scatter_kernel', 'radix_scatter'),
+    ('radix_hist_kernel', 'radix_hist'), ('radix_scan_kernel', 'radix_scan'),
+    ('cell_ranges_kernel', 'cell_ranges'), ('init_meta', 'init_meta'),
+)
+CALIBRATOR_BYTES = 512 << 20  # the --mode kernels device copy
+
+
+def fold_pmc(fetch_csv, write_csv, config):
+    """Fold two ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` runs of
+    ``--mode kernels`` into HBM bytes per launch for each library kernel.
+
+    Both counters read in KiB per dispatch.  Each is scaled by the factor that
+    makes the calibrator (a plain 512 MiB device-to-device copy, the largest
+    ``copyBuffer`` dispatches of the run) read exactly 512 MiB and write
+    exactly 512 MiB."""
+    import csv
+
+    def load(path, counter):
+        per = {}
+        cal = []
+        for r in csv.DictReader(open(path)):
+            if r['Counter_Name'] != counter:
+                continue
+            name, v = r['Kernel_Name'], float(r['Counter_Value'])
+            if 'copyBuffer' in name:
+                cal.append(v)
+                continue
+            for dev_name, timer in KERNEL_TIMER_NAMES:
+                if dev_name in name:
+                    per.setdefault(timer, []).append(v)
+                    break
+        cal = sorted(cal)[-3:]
+        if not cal:
+            raise SystemExit(f'{path}: no calibrator copy dispatches found')
+        factor = (CALIBRATOR_BYTES / 1024) / statistics.mean(cal)
+        return {k: statistics.mean(v) for k, v in per.items()}, factor, statistics.mean(cal)
+
+    fetch, ff, fcal = load(fetch_csv, 'FETCH_SIZE')
+    write, wf, wcal = load(write_csv, 'WRITE_SIZE')
+    kernels = {}
+    for k in sorted(set(fetch) | set(write)):
+        f_kib, w_kib = fetch.get(k, 0.0), write.get(k, 0.0)
+        kernels[k] = {'fetch_kib': round(f_kib, 1), 'write_kib': round(w_kib, 1),
+                      'traffic_bytes': int(round((f_kib * ff + w_kib * wf) * 1024))}
+    out = {
+        'config': config,
+        'calibration': {'copy_bytes': CALIBRATOR_BYTES, 'fetch_kib': round(fcal, 1),
+                        'write_kib': round(wcal, 1), 'fetch_factor': round(ff, 4),
+                        'write_factor': round(wf, 4)},
+        'kernels': kernels,
+    }
+    path = ROOT / 'profiles' / f'traffic_{config}.json'
+    path.write_text(json.dumps(out, indent=1) + '\n')
+    print(json.dumps(out, indent=1))
+
+
 def make_inputs(pkg, name, device):
     from bevfusion_triton_amd import synthetic
 
@@ -102,7 +163,13 @@ def main():
     ap.add_argument('--mode', default='bench', choices=['bench', 'kernels'],
                     help="'kernels': run --steps plain fwd+bwd steps and a 512 MiB device copy "
                          '(the traffic calibrator for rocprofv3 --pmc passes), print nothing')
+    ap.add_argument('--fold-pmc', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
+                    help='fold the counter_collection.csv files of a FETCH_SIZE and a WRITE_SIZE '
+                         'pass of --mode kernels into profiles/traffic_<config>.json (no GPU)')
     args = ap.parse_args()
+    if args.fold_pmc:
+        fold_pmc(*args.fold_pmc, args.config)
+        return
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}): the bev_pool path '
               'shards by batch with no collective; run one process per GPU.', file=sys.stderr)
@@ -230,7 +297,7 @@ def main():
     tfile = ROOT / 'profiles' / f'traffic_{args.config}.json'
     if tfile.exists():
         t = json.loads(tfile.read_text())
-        traffic = t.get('kernels', {}).get(dom)
+        traffic = t.get('kernels', {}).get(dom, {}).get('traffic_bytes')
 
     result = {
         'metric': METRIC,
