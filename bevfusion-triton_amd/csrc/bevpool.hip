@@ -59,10 +59,43 @@ constexpr int kWaveItems = 64 * kItems;    // 1024 keys per wave in the scatter
 constexpr int kMaxDigitBits = 10;
 constexpr int kMaxRadix = 1 << kMaxDigitBits;
 constexpr int kCellTile = 64;              // cells per transpose tile
+constexpr int kTileChannels = 128;         // max channels per transpose pass
+
+// 16- and 8-byte integer vectors.  HIP's uint4 struct blocks register
+// promotion.  Float vectors are avoided on purpose: with packed fp32 ops
+// disabled, hipcc 7.2 lowered a <2 x float> add of a 64-bit LDS load into two
+// scalar adds that both read the low half.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #ifndef BEVPOOL_RANGE_POINTS
 #define BEVPOOL_RANGE_POINTS 512
 #endif
 constexpr int64_t kRangePoints = BEVPOOL_RANGE_POINTS;  // nominal sorted points per forward range
+#ifndef BEVPOOL_XCD_MAP
+#define BEVPOOL_XCD_MAP 1
+#endif
+constexpr int kXcds = 8;                   // MI355X: 8 XCDs, one L2 each
+
+// Workgroup i of a launch runs on XCD i % 8.  xcd_chunk maps it to chunk
+// (i % 8) * (n / 8) + i / 8 of a grid of n workgroups (n a multiple of 8,
+// padded by xcd_grid), so each XCD walks one contiguous eighth of the
+// chunks and neighbouring chunks share that XCD's L2.  A bijection on [0, n).
+__device__ __forceinline__ int64_t xcd_chunk(int64_t i, int64_t n) {
+#if BEVPOOL_XCD_MAP
+  return (i % kXcds) * (n / kXcds) + i / kXcds;
+#else
+  (void)n;
+  return i;
+#endif
+}
+
+inline unsigned xcd_grid(int64_t blocks) {
+#if BEVPOOL_XCD_MAP
+  return unsigned((blocks + kXcds - 1) / kXcds * kXcds);
+#else
+  return unsigned(blocks);
+#endif
+}
 
 // ---------------------------------------------------------------------------
 // error reporting
@@ -178,6 +211,7 @@ struct F32 {
   using raw = uint32_t;
   __device__ static float load(const uint32_t *p) { return __builtin_bit_cast(float, *p); }
   __device__ static void store(uint32_t *p, float v) { *p = __builtin_bit_cast(uint32_t, v); }
+  __device__ static uint32_t to_raw(float v) { return __builtin_bit_cast(uint32_t, v); }
 };
 struct F16 {
   using raw = uint16_t;
@@ -187,6 +221,7 @@ struct F16 {
   __device__ static void store(uint16_t *p, float v) {
     *p = __builtin_bit_cast(uint16_t, _Float16(v));
   }
+  __device__ static uint16_t to_raw(float v) { return __builtin_bit_cast(uint16_t, _Float16(v)); }
 };
 struct BF16 {
   using raw = uint16_t;
@@ -194,15 +229,13 @@ struct BF16 {
     return __builtin_bit_cast(float, uint32_t(*p) << 16);
   }
   // round to nearest even; NaN -> canonical quiet NaN (torch's c10::BFloat16)
-  __device__ static void store(uint16_t *p, float v) {
+  __device__ static uint16_t to_raw(float v) {
     uint32_t u = __builtin_bit_cast(uint32_t, v);
-    if ((u & 0x7fffffffu) > 0x7f800000u) {
-      *p = 0x7fc0;
-      return;
-    }
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
     u += 0x7fffu + ((u >> 16) & 1u);
-    *p = uint16_t(u >> 16);
+    return uint16_t(u >> 16);
   }
+  __device__ static void store(uint16_t *p, float v) { *p = to_raw(v); }
 };
 
 // ---------------------------------------------------------------------------
@@ -555,7 +588,7 @@ __global__ __launch_bounds__(kThreads) void accum_rows_kernel(
   int *rk = reinterpret_cast<int *>(smem + R * CB);  // R + 1 ints
   const int tid = threadIdx.x;
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
-  const int64_t r0 = int64_t(blockIdx.x) * P;
+  const int64_t r0 = xcd_chunk(blockIdx.x, gridDim.x) * P;
   if (r0 >= n) return;
   const int64_t s = snap_to_cell(r0, n, keys, cend);
   const int64_t e = snap_to_cell(r0 + P < n ? r0 + P : n, n, keys, cend);
@@ -633,7 +666,6 @@ constexpr int kPipeThreads = 64 * kSummers + kLoaders;
 static_assert(kStageRows <= 64 && (kStageRows & (kStageRows - 1)) == 0, "stage rows");
 
 // native 16-byte vector (register-promotable, unlike the HIP uint4 wrapper)
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct PipeRange {
   int64_t s, e;  // sorted positions [s, e)
@@ -837,7 +869,7 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
   const uint32_t *kw = reinterpret_cast<const uint32_t *>(keys);
 
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
-  const int64_t r0 = int64_t(blockIdx.x) * P;
+  const int64_t r0 = xcd_chunk(blockIdx.x, gridDim.x) * P;
   if (r0 >= n) return;
   PipeRange pr;
   pr.s = snap_to_cell(r0, n, keys, cend);
@@ -909,43 +941,122 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
   }
 }
 
-// acc rows (cell-major fp32) -> out (channel-first, dtype T), tile of 64 cells
-// x 64 channels through LDS; empty cells are written as 0.
-template <typename T>
+// ---------------------------------------------------------------------------
+// transposes between cell-major rows and the channel-first BEV
+// ---------------------------------------------------------------------------
+// A tile is 64 consecutive cells (ranks); rows are staged in LDS as
+// [cell][channel] with a pitch of CT + 1 elements, CT = channels per pass.
+// On the channel-first side each thread moves 4 consecutive cells of one
+// channel: one 16-byte (fp32) or 8-byte (16-bit) access when kVecBev (n_xy,
+// the b/z/c strides and the base are multiples of 4 elements, so 4 cells
+// starting at a multiple of 4 share a (b, z) plane and are contiguous), else
+// one access per cell.  On the row side kVecRow moves 16-byte pieces of a row
+// (C * element size a multiple of 16).
+
+// Offset of cell `cell` (< 2^31) in a channel-first (b, c, z, xy) tensor
+// without the channel term.
+__device__ __forceinline__ int64_t cell_offset(uint32_t cell, uint32_t n_z, uint32_t n_xy,
+                                               int64_t sb, int64_t sz) {
+  const uint32_t per_b = n_z * n_xy;
+  const uint32_t b = cell / per_b, rem = cell - b * per_b;
+  const uint32_t z = rem / n_xy, xy = rem - z * n_xy;
+  return int64_t(b) * sb + int64_t(z) * sz + int64_t(xy);
+}
+
+// Per-tile cell table in LDS: occupied flag and channel-first offset (-1 past
+// the last cell).  Returns whether any cell of the tile is occupied.
+__device__ __forceinline__ bool load_tile_cells(int64_t cell0, int64_t n_cells,
+                                                const int32_t *__restrict__ cstart,
+                                                const int32_t *__restrict__ cend, int n_z,
+                                                int64_t n_xy, int64_t sb, int64_t sz, int *occ,
+                                                int64_t *off) {
+  const int tid = threadIdx.x;
+  int mine = 0;
+  if (tid < kCellTile) {
+    const int64_t cell = cell0 + tid;
+    if (cell < n_cells) {
+      mine = cend[cell] > cstart[cell] ? 1 : 0;
+      off[tid] = cell_offset(uint32_t(cell), uint32_t(n_z), uint32_t(n_xy), sb, sz);
+    } else {
+      off[tid] = -1;
+    }
+    occ[tid] = mine;
+  }
+  return __syncthreads_or(mine) != 0;
+}
+
+// acc rows (cell-major fp32, written for occupied cells only) -> out
+// (channel-first, dtype T); empty cells are written as 0.  The tile holds the
+// raw fp32 bits: only occupied rows are staged, and a staged 16-byte piece is
+// never converted lane by lane to float (hipcc 7.2 with packed fp32 ops
+// disabled folded bit casts of lanes y/z/w of such a vector into lane x).
+template <typename T, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
-    const float *__restrict__ acc, int C, const int32_t *__restrict__ cstart,
+    const float *__restrict__ acc, int C, int CT, const int32_t *__restrict__ cstart,
     const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
     int64_t sc, int64_t sz, typename T::raw *__restrict__ out) {
-  __shared__ float tile[kCellTile][kCellTile + 1];
+  using raw = typename T::raw;
+  extern __shared__ uint32_t tile_bits[];  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
   __shared__ int64_t off[kCellTile];
   const int tid = threadIdx.x;
   const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
-  if (tid < kCellTile) {
-    const int64_t cell = cell0 + tid;
-    occ[tid] = (cell < n_cells && cend[cell] > cstart[cell]) ? 1 : 0;
-    if (cell < n_cells) {
-      const int64_t per_b = int64_t(n_z) * n_xy;
-      const int64_t b = cell / per_b, rem = cell - b * per_b;
-      const int64_t z = rem / n_xy, xy = rem - z * n_xy;
-      off[tid] = b * sb + z * sz + xy;
-    } else {
-      off[tid] = -1;
-    }
-  }
-  __syncthreads();
-  for (int c0 = 0; c0 < C; c0 += kCellTile) {
-    const int cb = C - c0 < kCellTile ? C - c0 : kCellTile;
-    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
-      const int t = idx >> 6, c = idx & 63;
-      float v = 0.0f;
-      if (c < cb && occ[t]) v = acc[(cell0 + t) * C + c0 + c];
-      tile[t][c] = v;
+  const bool any = load_tile_cells(cell0, n_cells, cstart, cend, n_z, n_xy, sb, sz, occ, off);
+  const uint32_t *accb = reinterpret_cast<const uint32_t *>(acc);
+  const int pitch = CT + 1;
+  for (int c0 = 0; c0 < C; c0 += CT) {
+    const int cb = C - c0 < CT ? C - c0 : CT;
+    if (any) {
+      if (kVecRow) {
+        const uint32_t q = uint32_t(cb) >> 2;  // 16-byte pieces per row
+        for (uint32_t i = tid; i < kCellTile * q; i += kThreads) {
+          const uint32_t t = i / q, k = i - t * q;
+          if (occ[t]) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(accb + (cell0 + t) * C + c0 + 4 * k);
+            uint32_t *d = tile_bits + t * pitch + 4 * k;
+            d[0] = v.x;
+            d[1] = v.y;
+            d[2] = v.z;
+            d[3] = v.w;
+          }
+        }
+      } else {
+        for (uint32_t i = tid; i < uint32_t(kCellTile * cb); i += kThreads) {
+          const uint32_t t = i / uint32_t(cb), c = i - t * uint32_t(cb);
+          if (occ[t]) tile_bits[t * pitch + c] = accb[(cell0 + t) * C + c0 + c];
+        }
+      }
     }
     __syncthreads();
-    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
-      const int c = idx >> 6, t = idx & 63;
-      if (c < cb && off[t] >= 0) T::store(out + off[t] + int64_t(c0 + c) * sc, tile[t][c]);
+    for (int i = tid; i < cb * (kCellTile / 4); i += kThreads) {
+      const int c = i >> 4, j = (i & 15) * 4;
+      raw r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t b = (any && occ[j + u]) ? tile_bits[(j + u) * pitch + c] : 0u;
+        r[u] = T::to_raw(__builtin_bit_cast(float, b));
+      }
+      if (kVecBev) {
+        if (off[j] < 0) continue;
+        raw *dst = out + off[j] + int64_t(c0 + c) * sc;
+        if constexpr (sizeof(raw) == 4) {
+          u32x4 w;
+          w.x = r[0];
+          w.y = r[1];
+          w.z = r[2];
+          w.w = r[3];
+          *reinterpret_cast<u32x4 *>(dst) = w;
+        } else {
+          u32x2 w;
+          w.x = uint32_t(r[0]) | (uint32_t(r[1]) << 16);
+          w.y = uint32_t(r[2]) | (uint32_t(r[3]) << 16);
+          *reinterpret_cast<u32x2 *>(dst) = w;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (off[j + u] >= 0) out[off[j + u] + int64_t(c0 + c) * sc] = r[u];
+      }
     }
     __syncthreads();
   }
@@ -956,40 +1067,76 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
 // ---------------------------------------------------------------------------
 
 // grad (channel-first, any b/c/z strides, xy contiguous) -> cell-major rows of
-// the occupied cells (raw bits copied).
-template <typename TR>
+// the occupied cells (raw bits copied); tiles without an occupied cell exit.
+template <typename TR, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
-    const TR *__restrict__ grad, int C, const int32_t *__restrict__ cstart,
+    const TR *__restrict__ grad, int C, int CT, const int32_t *__restrict__ cstart,
     const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
     int64_t sc, int64_t sz, TR *__restrict__ rows) {
-  __shared__ TR tile[kCellTile][kCellTile + 1];
+  extern __shared__ u32x4 smem_b2r[];
+  TR *tile = reinterpret_cast<TR *>(smem_b2r);  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
   __shared__ int64_t off[kCellTile];
   const int tid = threadIdx.x;
   const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
-  int mine = 0;
-  if (tid < kCellTile) {
-    const int64_t cell = cell0 + tid;
-    mine = (cell < n_cells && cend[cell] > cstart[cell]) ? 1 : 0;
-    occ[tid] = mine;
-    if (mine) {
-      const int64_t per_b = int64_t(n_z) * n_xy;
-      const int64_t b = cell / per_b, rem = cell - b * per_b;
-      const int64_t z = rem / n_xy, xy = rem - z * n_xy;
-      off[tid] = b * sb + z * sz + xy;
-    }
-  }
-  if (!__syncthreads_or(mine)) return;  // no occupied cell: nothing to read
-  for (int c0 = 0; c0 < C; c0 += kCellTile) {
-    const int cb = C - c0 < kCellTile ? C - c0 : kCellTile;
-    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
-      const int c = idx >> 6, t = idx & 63;
-      if (c < cb && occ[t]) tile[t][c] = grad[off[t] + int64_t(c0 + c) * sc];
+  if (!load_tile_cells(cell0, n_cells, cstart, cend, n_z, n_xy, sb, sz, occ, off)) return;
+  const int pitch = CT + 1;
+  constexpr int kPer = 16 / int(sizeof(TR));  // elements per 16-byte row piece
+  for (int c0 = 0; c0 < C; c0 += CT) {
+    const int cb = C - c0 < CT ? C - c0 : CT;
+    for (int i = tid; i < cb * (kCellTile / 4); i += kThreads) {
+      const int c = i >> 4, j = (i & 15) * 4;
+      if (!(occ[j] | occ[j + 1] | occ[j + 2] | occ[j + 3])) continue;
+      TR v[4];
+      if (kVecBev) {
+        const TR *src = grad + off[j] + int64_t(c0 + c) * sc;
+        if constexpr (sizeof(TR) == 4) {
+          const u32x4 w = *reinterpret_cast<const u32x4 *>(src);
+          v[0] = w.x;
+          v[1] = w.y;
+          v[2] = w.z;
+          v[3] = w.w;
+        } else {
+          const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
+          v[0] = TR(w.x);
+          v[1] = TR(w.x >> 16);
+          v[2] = TR(w.y);
+          v[3] = TR(w.y >> 16);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          v[u] = occ[j + u] ? grad[off[j + u] + int64_t(c0 + c) * sc] : TR(0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) tile[(j + u) * pitch + c] = v[u];
     }
     __syncthreads();
-    for (int idx = tid; idx < kCellTile * kCellTile; idx += kThreads) {
-      const int t = idx >> 6, c = idx & 63;
-      if (c < cb && occ[t]) rows[(cell0 + t) * C + c0 + c] = tile[t][c];
+    if (kVecRow) {
+      const uint32_t q = uint32_t(cb) / kPer;  // 16-byte pieces per row
+      for (uint32_t i = tid; i < kCellTile * q; i += kThreads) {
+        const uint32_t t = i / q, k = i - t * q;
+        if (!occ[t]) continue;
+        const TR *srow = tile + t * pitch + kPer * k;
+        u32x4 w;
+        if constexpr (sizeof(TR) == 4) {
+          w.x = srow[0];
+          w.y = srow[1];
+          w.z = srow[2];
+          w.w = srow[3];
+        } else {
+          w.x = uint32_t(srow[0]) | (uint32_t(srow[1]) << 16);
+          w.y = uint32_t(srow[2]) | (uint32_t(srow[3]) << 16);
+          w.z = uint32_t(srow[4]) | (uint32_t(srow[5]) << 16);
+          w.w = uint32_t(srow[6]) | (uint32_t(srow[7]) << 16);
+        }
+        *reinterpret_cast<u32x4 *>(rows + (cell0 + t) * C + c0 + kPer * k) = w;
+      }
+    } else {
+      for (uint32_t i = tid; i < uint32_t(kCellTile * cb); i += kThreads) {
+        const uint32_t t = i / uint32_t(cb), c = i - t * uint32_t(cb);
+        if (occ[t]) rows[(cell0 + t) * C + c0 + c] = tile[t * pitch + c];
+      }
     }
     __syncthreads();
   }
@@ -1011,7 +1158,7 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const V *__restrict__ rows, int vpr, const int32_t *__restrict__ rank, int64_t n_points,
     V *__restrict__ xg, int64_t xg_ld) {
   const int64_t total = n_points * vpr;
-  const int64_t base = int64_t(blockIdx.x) * (kThreads * kGatherPer) + threadIdx.x;
+  const int64_t base = xcd_chunk(blockIdx.x, gridDim.x) * (kThreads * kGatherPer) + threadIdx.x;
 #pragma unroll
   for (int j = 0; j < kGatherPer; ++j) {
     const int64_t i = base + j * kThreads;
@@ -1104,6 +1251,15 @@ int check_index_args(int64_t n_points, int64_t n_cells, const void *rank, const 
 }
 
 size_t dtype_size(int32_t dtype) { return dtype == BEVPOOL_F32 ? 4 : 2; }
+
+// 4 consecutive cells of one channel of a channel-first tensor form one
+// aligned 4-element vector when n_xy and the b/c/z strides are multiples of
+// 4 and the base is aligned to 4 elements (tiles start at multiples of 64).
+bool bev_vec_ok(const void *base, size_t es, int64_t n_xy, int64_t sb, int64_t sc,
+                int64_t sz) {
+  return n_xy % 4 == 0 && sb % 4 == 0 && sc % 4 == 0 && sz % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(base) % (4 * es) == 0;
+}
 
 template <typename T, int kCPL>
 int launch_accum_pipe_t(int slots, unsigned grid, size_t smem, hipStream_t s, const char *x,
@@ -1376,7 +1532,7 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
     const size_t es = dtype_size(dtype);
     const bool vec16 = (size_t(C) * es) % 16 == 0 && (size_t(feats_row_stride) * es) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(feats) % 16 == 0;
-    const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
+    const unsigned grid = xcd_grid(ceil_div(n_points, kRangePoints));
     if (vec16) {
       // channel block of at most 384 bytes per row: <= 6 16-byte slots per thread per
       // stage and two stages + ranks in <= 48.5 KB of LDS (three blocks per CU)
@@ -1419,24 +1575,34 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
     }
   }
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
+  const int CT = C < kTileChannels ? C : kTileChannels;
+  const size_t es = dtype_size(dtype);
+  const size_t smem = size_t(kCellTile) * size_t(CT + 1) * sizeof(uint32_t);
+  const bool vrow = (C % 4 == 0) && (CT % 4 == 0) && (reinterpret_cast<uintptr_t>(acc) % 16 == 0);
+  const bool vbev = bev_vec_ok(out, es, n_xy, out_stride_b, out_stride_c, out_stride_z);
   LaunchTimer t("rows_to_bev", s);
+#define BEVPOOL_R2B(T, VR, VB)                                                                 \
+  hipLaunchKernelGGL((rows_to_bev_kernel<T, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,    \
+                     acc, C, CT, cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b,       \
+                     out_stride_c, out_stride_z, static_cast<T::raw *>(out))
+#define BEVPOOL_R2B_T(T)                                                                       \
+  if (vrow && vbev) BEVPOOL_R2B(T, true, true);                                               \
+  else if (vrow) BEVPOOL_R2B(T, true, false);                                                 \
+  else if (vbev) BEVPOOL_R2B(T, false, true);                                                 \
+  else BEVPOOL_R2B(T, false, false);
   switch (dtype) {
     case BEVPOOL_F32:
-      hipLaunchKernelGGL(rows_to_bev_kernel<F32>, dim3(tiles), dim3(kThreads), 0, s, acc, C,
-                         cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b, out_stride_c,
-                         out_stride_z, static_cast<uint32_t *>(out));
+      BEVPOOL_R2B_T(F32)
       break;
     case BEVPOOL_F16:
-      hipLaunchKernelGGL(rows_to_bev_kernel<F16>, dim3(tiles), dim3(kThreads), 0, s, acc, C,
-                         cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b, out_stride_c,
-                         out_stride_z, static_cast<uint16_t *>(out));
+      BEVPOOL_R2B_T(F16)
       break;
     default:
-      hipLaunchKernelGGL(rows_to_bev_kernel<BF16>, dim3(tiles), dim3(kThreads), 0, s, acc, C,
-                         cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b, out_stride_c,
-                         out_stride_z, static_cast<uint16_t *>(out));
+      BEVPOOL_R2B_T(BF16)
       break;
   }
+#undef BEVPOOL_R2B_T
+#undef BEVPOOL_R2B
   return check_launch("rows_to_bev");
 }
 
@@ -1471,18 +1637,30 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
   int st;
   {
+    const int CT = C < kTileChannels ? C : kTileChannels;
+    const size_t smem = size_t(kCellTile) * size_t(CT + 1) * es;
+    const bool vrow = (size_t(C) * es % 16 == 0) && (size_t(CT) * es % 16 == 0) &&
+                      (reinterpret_cast<uintptr_t>(scratch) % 16 == 0);
+    const bool vbev =
+        bev_vec_ok(grad, es, n_xy, grad_stride_b, grad_stride_c, grad_stride_z);
     LaunchTimer t("bev_to_rows", s);
+#define BEVPOOL_B2R(TR, VR, VB)                                                                \
+  hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,   \
+                     static_cast<const TR *>(grad), C, CT, cell_start, cell_end, n_cells, n_z, \
+                     n_xy, grad_stride_b, grad_stride_c, grad_stride_z,                        \
+                     static_cast<TR *>(scratch))
+#define BEVPOOL_B2R_T(TR)                                                                      \
+  if (vrow && vbev) BEVPOOL_B2R(TR, true, true);                                              \
+  else if (vrow) BEVPOOL_B2R(TR, true, false);                                                \
+  else if (vbev) BEVPOOL_B2R(TR, false, true);                                                \
+  else BEVPOOL_B2R(TR, false, false);
     if (es == 4) {
-      hipLaunchKernelGGL(bev_to_rows_kernel<uint32_t>, dim3(tiles), dim3(kThreads), 0, s,
-                         static_cast<const uint32_t *>(grad), C, cell_start, cell_end, n_cells,
-                         n_z, n_xy, grad_stride_b, grad_stride_c, grad_stride_z,
-                         static_cast<uint32_t *>(scratch));
+      BEVPOOL_B2R_T(uint32_t)
     } else {
-      hipLaunchKernelGGL(bev_to_rows_kernel<uint16_t>, dim3(tiles), dim3(kThreads), 0, s,
-                         static_cast<const uint16_t *>(grad), C, cell_start, cell_end, n_cells,
-                         n_z, n_xy, grad_stride_b, grad_stride_c, grad_stride_z,
-                         static_cast<uint16_t *>(scratch));
+      BEVPOOL_B2R_T(uint16_t)
     }
+#undef BEVPOOL_B2R_T
+#undef BEVPOOL_B2R
     if ((st = check_launch("bev_to_rows"))) return st;
   }
   const size_t row_bytes = size_t(C) * es;
@@ -1492,7 +1670,7 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
   LaunchTimer t("gather_rows", s);
   const int vpr = vec16 ? int(row_bytes / 16) : int(C);
   const int64_t total = n_points * vpr;
-  const unsigned grid = unsigned(ceil_div(total, int64_t(kThreads) * kGatherPer));
+  const unsigned grid = xcd_grid(ceil_div(total, int64_t(kThreads) * kGatherPer));
   const bool narrow = total < (int64_t(1) << 32);
 #define BEVPOOL_GATHER(V, NARROW, LD)                                                          \
   hipLaunchKernelGGL((gather_rows_kernel<V, NARROW>), dim3(grid), dim3(kThreads), 0, s,        \
