@@ -588,7 +588,7 @@ __global__ __launch_bounds__(kThreads) void accum_rows_kernel(
   int *rk = reinterpret_cast<int *>(smem + R * CB);  // R + 1 ints
   const int tid = threadIdx.x;
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
-  const int64_t r0 = xcd_chunk(blockIdx.x, gridDim.x) * P;
+  const int64_t r0 = int64_t(blockIdx.x) * P;
   if (r0 >= n) return;
   const int64_t s = snap_to_cell(r0, n, keys, cend);
   const int64_t e = snap_to_cell(r0 + P < n ? r0 + P : n, n, keys, cend);
@@ -869,7 +869,7 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
   const uint32_t *kw = reinterpret_cast<const uint32_t *>(keys);
 
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
-  const int64_t r0 = xcd_chunk(blockIdx.x, gridDim.x) * P;
+  const int64_t r0 = int64_t(blockIdx.x) * P;
   if (r0 >= n) return;
   PipeRange pr;
   pr.s = snap_to_cell(r0, n, keys, cend);
@@ -1068,17 +1068,47 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
 
 // grad (channel-first, any b/c/z strides, xy contiguous) -> cell-major rows of
 // the occupied cells (raw bits copied); tiles without an occupied cell exit.
+//
+// The first warm_blocks blocks instead read the rank array (16-byte pieces,
+// kWarmPer per thread), so that the gather that follows finds it in the
+// memory-side cache: its rank -> row -> store chain is latency bound, and a
+// rank array evicted by the forward pass's traffic costs it ~50% of its speed.
+constexpr int kWarmPer = 16;
+
+__device__ __forceinline__ void warm_pieces(const u32x4 *__restrict__ a, int64_t n16,
+                                            int64_t wb, uint32_t *__restrict__ sink) {
+  const int64_t base = wb * (kThreads * kWarmPer) + threadIdx.x;
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < kWarmPer; ++j) {
+    const int64_t i = base + int64_t(j) * kThreads;
+    if (i < n16) {
+      const u32x4 v = a[i];
+      const uint32_t m01 = max(v.x + 1u, v.y + 1u), m23 = max(v.z + 1u, v.w + 1u);
+      m = max(m, max(m01, m23));
+    }
+  }
+  // ranks lie in [-1, 2^31 - 1), so rank + 1 <= 2^31: this store never runs,
+  // it only keeps the loads alive
+  if (m > 0x80000000u) sink[0] = m;
+}
+
 template <typename TR, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
     const TR *__restrict__ grad, int C, int CT, const int32_t *__restrict__ cstart,
     const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
-    int64_t sc, int64_t sz, TR *__restrict__ rows) {
+    int64_t sc, int64_t sz, TR *__restrict__ rows, const u32x4 *__restrict__ warm,
+    int64_t warm_n16, int warm_blocks) {
+  if (int(blockIdx.x) < warm_blocks) {
+    warm_pieces(warm, warm_n16, blockIdx.x, reinterpret_cast<uint32_t *>(rows));
+    return;
+  }
   extern __shared__ u32x4 smem_b2r[];
   TR *tile = reinterpret_cast<TR *>(smem_b2r);  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
   __shared__ int64_t off[kCellTile];
   const int tid = threadIdx.x;
-  const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
+  const int64_t cell0 = int64_t(blockIdx.x - warm_blocks) * kCellTile;
   if (!load_tile_cells(cell0, n_cells, cstart, cend, n_z, n_xy, sb, sz, occ, off)) return;
   const int pitch = CT + 1;
   constexpr int kPer = 16 / int(sizeof(TR));  // elements per 16-byte row piece
@@ -1144,12 +1174,16 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
 
 // x_grad[p, :] = rows[rank[p], :] (kept) or 0 (dropped); point order, so the
 // writes stream.  V is a 16-byte vector when rows allow it, else one element.
-// Each thread copies kPer vectors spaced kThreads apart (coalesced); the
-// destination is written with non-temporal stores (it is not read again
-// here, and keeping it out of L2 leaves room for the gradient rows that are
-// re-read once per point of their cell).  kNarrow: indices fit in 32 bits.
+// Each thread copies kGatherPer vectors spaced kThreads apart (coalesced),
+// blocks walk XCD-contiguous chunks (an XCD's points map to a compact set of
+// cells, whose rows then stay in its L2), and the destination is written
+// with non-temporal stores (it is not read again here, and keeping it out of
+// L2 leaves room for the gradient rows).  Each piece is a dependent chain
+// rank -> row -> store, so the kernel relies on bev_to_rows_kernel having
+// pulled the rank array into the memory-side cache.  kNarrow: indices fit in
+// 32 bits.
 #ifndef BEVPOOL_GATHER_PER
-#define BEVPOOL_GATHER_PER 4
+#define BEVPOOL_GATHER_PER 1
 #endif
 constexpr int kGatherPer = BEVPOOL_GATHER_PER;
 
@@ -1532,7 +1566,9 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
     const size_t es = dtype_size(dtype);
     const bool vec16 = (size_t(C) * es) % 16 == 0 && (size_t(feats_row_stride) * es) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(feats) % 16 == 0;
-    const unsigned grid = xcd_grid(ceil_div(n_points, kRangePoints));
+    // plain block order: ranges that run at the same time then read rows from
+    // one window of the feature tensor (an XCD-contiguous order measured slower)
+    const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
     if (vec16) {
       // channel block of at most 384 bytes per row: <= 6 16-byte slots per thread per
       // stage and two stages + ranks in <= 48.5 KB of LDS (three blocks per CU)
@@ -1644,11 +1680,15 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
     const bool vbev =
         bev_vec_ok(grad, es, n_xy, grad_stride_b, grad_stride_c, grad_stride_z);
     LaunchTimer t("bev_to_rows", s);
+    const bool rank16 = reinterpret_cast<uintptr_t>(rank) % 16 == 0;
+    const int64_t warm_n16 = rank16 ? n_points * 4 / 16 : 0;
+    const int warm_blocks = int(ceil_div(warm_n16, int64_t(kThreads) * kWarmPer));
 #define BEVPOOL_B2R(TR, VR, VB)                                                                \
-  hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,   \
-                     static_cast<const TR *>(grad), C, CT, cell_start, cell_end, n_cells, n_z, \
-                     n_xy, grad_stride_b, grad_stride_c, grad_stride_z,                        \
-                     static_cast<TR *>(scratch))
+  hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles + warm_blocks),              \
+                     dim3(kThreads), smem, s, static_cast<const TR *>(grad), C, CT, cell_start,  \
+                     cell_end, n_cells, n_z, n_xy, grad_stride_b, grad_stride_c,               \
+                     grad_stride_z, static_cast<TR *>(scratch),                                \
+                     reinterpret_cast<const u32x4 *>(rank), warm_n16, warm_blocks)
 #define BEVPOOL_B2R_T(TR)                                                                      \
   if (vrow && vbev) BEVPOOL_B2R(TR, true, true);                                              \
   else if (vrow) BEVPOOL_B2R(TR, true, false);                                                \
