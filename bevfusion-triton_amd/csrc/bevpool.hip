@@ -23,6 +23,8 @@
 //   backward
 //     bev_to_rows_kernel<T>     channel-first grad tile -> cell-major rows
 //                               (occupied cells only) via LDS transpose
+//     gather_warm_kernel        reads the ranks (per XCD) and the occupied
+//                               rows once so the gather finds them cached
 //     gather_rows_kernel<V>     point-order streaming copy of each point's
 //                               cell row (zero rows for dropped points)
 //
@@ -53,9 +55,12 @@ namespace {
 // ---------------------------------------------------------------------------
 constexpr int kThreads = 256;              // threads per block, every kernel
 constexpr int kWaves = kThreads / 64;      // wave64 waves per block
-constexpr int kItems = 16;                 // keys per thread in sort kernels
-constexpr int kSortTile = kThreads * kItems;  // 4096 keys per sort block
-constexpr int kWaveItems = 64 * kItems;    // 1024 keys per wave in the scatter
+#ifndef BEVPOOL_SORT_ITEMS
+#define BEVPOOL_SORT_ITEMS 16
+#endif
+constexpr int kItems = BEVPOOL_SORT_ITEMS;    // keys per thread in sort kernels
+constexpr int kSortTile = kThreads * kItems;  // keys per sort block
+constexpr int kWaveItems = 64 * kItems;       // keys per wave in the scatter
 constexpr int kMaxDigitBits = 10;
 constexpr int kMaxRadix = 1 << kMaxDigitBits;
 constexpr int kCellTile = 64;              // cells per transpose tile
@@ -249,8 +254,12 @@ struct BF16 {
 __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
     const float *__restrict__ geom, int64_t n_points, int64_t gstride, int64_t ppb, float o0,
     float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
-    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits) {
+    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits,
+    int32_t *__restrict__ meta) {
   __shared__ int cnt[kMaxRadix];
+  if (blockIdx.x == 0 && threadIdx.x < BEVPOOL_META_LEN)  // nothing else touches meta here
+    meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
+  if (int(blockIdx.x) >= nblocks) return;  // the one block of an empty launch
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
@@ -1069,46 +1078,17 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
 // grad (channel-first, any b/c/z strides, xy contiguous) -> cell-major rows of
 // the occupied cells (raw bits copied); tiles without an occupied cell exit.
 //
-// The first warm_blocks blocks instead read the rank array (16-byte pieces,
-// kWarmPer per thread), so that the gather that follows finds it in the
-// memory-side cache: its rank -> row -> store chain is latency bound, and a
-// rank array evicted by the forward pass's traffic costs it ~50% of its speed.
-constexpr int kWarmPer = 16;
-
-__device__ __forceinline__ void warm_pieces(const u32x4 *__restrict__ a, int64_t n16,
-                                            int64_t wb, uint32_t *__restrict__ sink) {
-  const int64_t base = wb * (kThreads * kWarmPer) + threadIdx.x;
-  uint32_t m = 0;
-#pragma unroll
-  for (int j = 0; j < kWarmPer; ++j) {
-    const int64_t i = base + int64_t(j) * kThreads;
-    if (i < n16) {
-      const u32x4 v = a[i];
-      const uint32_t m01 = max(v.x + 1u, v.y + 1u), m23 = max(v.z + 1u, v.w + 1u);
-      m = max(m, max(m01, m23));
-    }
-  }
-  // ranks lie in [-1, 2^31 - 1), so rank + 1 <= 2^31: this store never runs,
-  // it only keeps the loads alive
-  if (m > 0x80000000u) sink[0] = m;
-}
-
 template <typename TR, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
     const TR *__restrict__ grad, int C, int CT, const int32_t *__restrict__ cstart,
     const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
-    int64_t sc, int64_t sz, TR *__restrict__ rows, const u32x4 *__restrict__ warm,
-    int64_t warm_n16, int warm_blocks) {
-  if (int(blockIdx.x) < warm_blocks) {
-    warm_pieces(warm, warm_n16, blockIdx.x, reinterpret_cast<uint32_t *>(rows));
-    return;
-  }
+    int64_t sc, int64_t sz, TR *__restrict__ rows) {
   extern __shared__ u32x4 smem_b2r[];
   TR *tile = reinterpret_cast<TR *>(smem_b2r);  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
   __shared__ int64_t off[kCellTile];
   const int tid = threadIdx.x;
-  const int64_t cell0 = int64_t(blockIdx.x - warm_blocks) * kCellTile;
+  const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
   if (!load_tile_cells(cell0, n_cells, cstart, cend, n_z, n_xy, sb, sz, occ, off)) return;
   const int pitch = CT + 1;
   constexpr int kPer = 16 / int(sizeof(TR));  // elements per 16-byte row piece
@@ -1172,6 +1152,94 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
   }
 }
 
+// Cache warm-up for gather_rows_kernel.  Each gather piece is a dependent
+// chain rank -> row -> store; with the rank array and the gradient rows
+// fetched from HBM while the gather's write stream saturates it, the chains
+// take about twice as long (measured 92 us vs 155-185 us at the det shape).
+// Rows written by bev_to_rows_kernel are not reliably kept by the caches, rows
+// that were read are, so this kernel reads both once:
+//   * blocks [0, 8 * per_xcd): block wb runs on XCD wb % 8 and reads a share
+//     of the ranks that XCD's gather blocks will need (the gather walks
+//     XCD-contiguous eighths of its pieces, xcd_span pieces each), so they are
+//     in that XCD's L2;
+//   * the other blocks read the rows of the occupied cells of kWarmCells
+//     consecutive cells each (16-byte pieces).
+// Nothing is written: the only store is guarded by `never`, a launch argument
+// that is always 0, which keeps the loads from being optimised away.
+#ifndef BEVPOOL_WARM_CELLS
+#define BEVPOOL_WARM_CELLS 512
+#endif
+constexpr int kWarmCells = BEVPOOL_WARM_CELLS;  // cells per row-warming block
+constexpr int kWarmBatch = 8;                   // loads in flight per thread
+
+struct GatherWarm {
+  const u32x4 *rank16;   // rank array as 16-byte pieces (null: skip)
+  int64_t n16;           // whole pieces in the array
+  int64_t xcd_span;      // gather pieces (vectors of xg) per XCD
+  int vpr;               // gather pieces per point
+  int per_xcd;           // rank blocks per XCD
+  const u32x4 *rows16;   // gradient rows as 16-byte pieces (null: skip)
+  int rowq;              // 16-byte pieces per row
+};
+
+// Warm-up work of block wb (< warm_blocks(w, tiles)); returns nothing, reads only.
+__device__ __forceinline__ void gather_warm_block(const GatherWarm &w, int wb, int64_t n_points,
+                                                  const int32_t *__restrict__ cstart,
+                                                  const int32_t *__restrict__ cend,
+                                                  int64_t n_cells, int never,
+                                                  uint32_t *__restrict__ sink) {
+  __shared__ int occ[kWarmCells];
+  const int rank_blocks = w.rank16 ? kXcds * w.per_xcd : 0;
+  uint32_t m = 0;
+  if (wb < rank_blocks) {
+    const int x = wb % kXcds, j = wb / kXcds;
+    // points [p0, p1) are gathered by XCD x; their ranks are pieces [q0, q1)
+    const int64_t p0 = int64_t(x) * w.xcd_span / w.vpr;
+    int64_t p1 = (int64_t(x + 1) * w.xcd_span + w.vpr - 1) / w.vpr;
+    p1 = p1 < n_points ? p1 : n_points;
+    const int64_t q0 = p0 / 4;
+    int64_t q1 = (p1 + 3) / 4;
+    q1 = q1 < w.n16 ? q1 : w.n16;
+    const int64_t share = (q1 - q0 + w.per_xcd - 1) / w.per_xcd;
+    const int64_t b0 = q0 + int64_t(j) * share;
+    int64_t b1 = b0 + share;
+    b1 = b1 < q1 ? b1 : q1;
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += kThreads) {
+      const u32x4 v = w.rank16[i];
+      m ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+  } else if (w.rows16) {
+    // kWarmCells consecutive cells per block: occupancy, then the occupied
+    // rows' pieces, kWarmBatch loads in flight per thread
+    const int64_t cell0 = int64_t(wb - rank_blocks) * kWarmCells;
+    for (int t = threadIdx.x; t < kWarmCells; t += kThreads) {
+      const int64_t cell = cell0 + t;
+      occ[t] = (cell < n_cells && cend[cell] > cstart[cell]) ? 1 : 0;
+    }
+    __syncthreads();
+    const uint32_t q = uint32_t(w.rowq);
+    const uint32_t n = kWarmCells * q;
+    for (uint32_t i0 = threadIdx.x; i0 < n; i0 += kThreads * kWarmBatch) {
+      u32x4 v[kWarmBatch];
+#pragma unroll
+      for (int b = 0; b < kWarmBatch; ++b) {
+        const uint32_t i = i0 + uint32_t(b) * kThreads < n ? i0 + uint32_t(b) * kThreads : n - 1;
+        const uint32_t t = i / q, k = i - t * q;
+        v[b] = occ[t] ? w.rows16[(cell0 + t) * q + k] : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int b = 0; b < kWarmBatch; ++b) m ^= v[b].x ^ v[b].y ^ v[b].z ^ v[b].w;
+    }
+  }
+  if (never) sink[threadIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kThreads) void gather_warm_kernel(
+    GatherWarm w, int64_t n_points, const int32_t *__restrict__ cstart,
+    const int32_t *__restrict__ cend, int64_t n_cells, int never, uint32_t *__restrict__ sink) {
+  gather_warm_block(w, int(blockIdx.x), n_points, cstart, cend, n_cells, never, sink);
+}
+
 // x_grad[p, :] = rows[rank[p], :] (kept) or 0 (dropped); point order, so the
 // writes stream.  V is a 16-byte vector when rows allow it, else one element.
 // Each thread copies kGatherPer vectors spaced kThreads apart (coalesced),
@@ -1179,20 +1247,37 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
 // cells, whose rows then stay in its L2), and the destination is written
 // with non-temporal stores (it is not read again here, and keeping it out of
 // L2 leaves room for the gradient rows).  Each piece is a dependent chain
-// rank -> row -> store, so the kernel relies on bev_to_rows_kernel having
-// pulled the rank array into the memory-side cache.  kNarrow: indices fit in
-// 32 bits.
+// rank -> row -> store, so the kernel runs after gather_warm_kernel has
+// pulled the ranks and the rows into the caches.  kNarrow: indices fit in 32
+// bits.
 #ifndef BEVPOOL_GATHER_PER
 #define BEVPOOL_GATHER_PER 1
+#endif
+#ifndef BEVPOOL_GATHER_NT
+#define BEVPOOL_GATHER_NT 1
+#endif
+#ifndef BEVPOOL_SEPARATE_WARM
+#define BEVPOOL_SEPARATE_WARM 0
 #endif
 constexpr int kGatherPer = BEVPOOL_GATHER_PER;
 
 template <typename V, bool kNarrow>
 __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const V *__restrict__ rows, int vpr, const int32_t *__restrict__ rank, int64_t n_points,
-    V *__restrict__ xg, int64_t xg_ld) {
+    V *__restrict__ xg, int64_t xg_ld, int warm_blocks, GatherWarm w,
+    const int32_t *__restrict__ cstart, const int32_t *__restrict__ cend, int64_t n_cells,
+    int never) {
+  // the first warm_blocks blocks (a multiple of 8, so XCD parity is kept)
+  // only pull ranks and rows into the caches ahead of the others
+  if (int(blockIdx.x) < warm_blocks) {
+    gather_warm_block(w, int(blockIdx.x), n_points, cstart, cend, n_cells, never,
+                      reinterpret_cast<uint32_t *>(xg));
+    return;
+  }
   const int64_t total = n_points * vpr;
-  const int64_t base = xcd_chunk(blockIdx.x, gridDim.x) * (kThreads * kGatherPer) + threadIdx.x;
+  const int64_t gb = int64_t(blockIdx.x) - warm_blocks;
+  const int64_t base =
+      xcd_chunk(gb, int64_t(gridDim.x) - warm_blocks) * (kThreads * kGatherPer) + threadIdx.x;
 #pragma unroll
   for (int j = 0; j < kGatherPer; ++j) {
     const int64_t i = base + j * kThreads;
@@ -1210,7 +1295,11 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
       const int r = rank[p];
       V v = V{};
       if (r >= 0) v = rows[int64_t(r) * vpr + q];
+#if BEVPOOL_GATHER_NT
       __builtin_nontemporal_store(v, xg + p * xg_ld + q);
+#else
+      xg[p * xg_ld + q] = v;
+#endif
     }
   }
 }
@@ -1382,20 +1471,16 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
     return fail(BEVPOOL_EINVAL, "bad geometry layout (row stride %lld, points/batch %lld)",
                 (long long)geom_row_stride, (long long)points_per_batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  {
-    LaunchTimer t("init_meta", s);
-    hipLaunchKernelGGL(init_meta_kernel, dim3(1), dim3(64), 0, s, meta);
-  }
-  if ((st = check_launch("init_meta"))) return st;
-  if (n_points == 0) return BEVPOOL_OK;
   const IndexLayout L = index_layout(n_points);
   const DigitPlan plan = plan_digits(n_cells);
   {
+    // also resets meta (block 0); an empty input still launches that block
     LaunchTimer t("quantize_geom", s);
-    hipLaunchKernelGGL(quantize_geom_kernel, dim3(unsigned(L.sort_blocks)), dim3(kThreads), 0, s,
-                       geom, n_points, geom_row_stride, points_per_batch, offset[0], offset[1],
-                       offset[2], dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,
-                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
+    const unsigned grid = L.sort_blocks > 0 ? unsigned(L.sort_blocks) : 1u;
+    hipLaunchKernelGGL(quantize_geom_kernel, dim3(grid), dim3(kThreads), 0, s, geom, n_points,
+                       geom_row_stride, points_per_batch, offset[0], offset[1], offset[2], dx[0],
+                       dx[1], dx[2], nx[0], nx[1], nx[2], rank, at<int32_t>(workspace, L.hist),
+                       int(L.sort_blocks), plan.bits[0], meta);
   }
   return check_launch("quantize_geom");
 }
@@ -1671,6 +1756,15 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t es = dtype_size(dtype);
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
+  // gather layout (decided first: the warm-up in bev_to_rows mirrors it)
+  const size_t row_bytes = size_t(C) * es;
+  const bool vec16 = (row_bytes % 16 == 0) && ((size_t(x_grad_row_stride) * es) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(x_grad) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(scratch) % 16 == 0);
+  const int vpr = vec16 ? int(row_bytes / 16) : int(C);
+  const int64_t total = n_points * vpr;
+  const unsigned grid = xcd_grid(ceil_div(total, int64_t(kThreads) * kGatherPer));
+  const bool narrow = total < (int64_t(1) << 32);
   int st;
   {
     const int CT = C < kTileChannels ? C : kTileChannels;
@@ -1680,15 +1774,11 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
     const bool vbev =
         bev_vec_ok(grad, es, n_xy, grad_stride_b, grad_stride_c, grad_stride_z);
     LaunchTimer t("bev_to_rows", s);
-    const bool rank16 = reinterpret_cast<uintptr_t>(rank) % 16 == 0;
-    const int64_t warm_n16 = rank16 ? n_points * 4 / 16 : 0;
-    const int warm_blocks = int(ceil_div(warm_n16, int64_t(kThreads) * kWarmPer));
 #define BEVPOOL_B2R(TR, VR, VB)                                                                \
-  hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles + warm_blocks),              \
-                     dim3(kThreads), smem, s, static_cast<const TR *>(grad), C, CT, cell_start,  \
-                     cell_end, n_cells, n_z, n_xy, grad_stride_b, grad_stride_c,               \
-                     grad_stride_z, static_cast<TR *>(scratch),                                \
-                     reinterpret_cast<const u32x4 *>(rank), warm_n16, warm_blocks)
+  hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,   \
+                     static_cast<const TR *>(grad), C, CT, cell_start, cell_end, n_cells, n_z, \
+                     n_xy, grad_stride_b, grad_stride_c, grad_stride_z,                        \
+                     static_cast<TR *>(scratch))
 #define BEVPOOL_B2R_T(TR)                                                                      \
   if (vrow && vbev) BEVPOOL_B2R(TR, true, true);                                              \
   else if (vrow) BEVPOOL_B2R(TR, true, false);                                                \
@@ -1703,19 +1793,42 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
 #undef BEVPOOL_B2R
     if ((st = check_launch("bev_to_rows"))) return st;
   }
-  const size_t row_bytes = size_t(C) * es;
-  const bool vec16 = (row_bytes % 16 == 0) && ((size_t(x_grad_row_stride) * es) % 16 == 0) &&
-                     (reinterpret_cast<uintptr_t>(x_grad) % 16 == 0) &&
-                     (reinterpret_cast<uintptr_t>(scratch) % 16 == 0);
+  // cache warm-up (see gather_warm_kernel): ranks per XCD + occupied rows
+  GatherWarm w{};
+  int rank_blocks = 0;
+  if (BEVPOOL_XCD_MAP && reinterpret_cast<uintptr_t>(rank) % 16 == 0 && n_points >= 4) {
+    w.rank16 = reinterpret_cast<const u32x4 *>(rank);
+    w.n16 = n_points / 4;
+    w.xcd_span = int64_t(grid / kXcds) * kThreads * kGatherPer;
+    w.vpr = vpr;
+    const int64_t pts = ceil_div(w.xcd_span, int64_t(vpr)) + 1;
+    w.per_xcd = int(ceil_div(ceil_div(pts, 4), int64_t(kThreads) * 16));  // <= 16 pieces/thread
+    rank_blocks = kXcds * w.per_xcd;
+  }
+  int row_blocks = 0;
+  if (BEVPOOL_XCD_MAP && vec16) {
+    w.rows16 = static_cast<const u32x4 *>(scratch);
+    w.rowq = vpr;
+    row_blocks = int(ceil_div(n_cells, kWarmCells));
+  }
+  int warm_blocks = rank_blocks + row_blocks;
+#if BEVPOOL_SEPARATE_WARM
+  if (warm_blocks > 0) {
+    LaunchTimer t("gather_warm", s);
+    hipLaunchKernelGGL(gather_warm_kernel, dim3(unsigned(warm_blocks)), dim3(kThreads), 0, s, w,
+                       n_points, cell_start, cell_end, n_cells, 0,
+                       static_cast<uint32_t *>(scratch));
+    if ((st = check_launch("gather_warm"))) return st;
+  }
+  warm_blocks = 0;
+#endif
+  warm_blocks = int(ceil_div(warm_blocks, kXcds) * kXcds);  // keep XCD parity
   LaunchTimer t("gather_rows", s);
-  const int vpr = vec16 ? int(row_bytes / 16) : int(C);
-  const int64_t total = n_points * vpr;
-  const unsigned grid = xcd_grid(ceil_div(total, int64_t(kThreads) * kGatherPer));
-  const bool narrow = total < (int64_t(1) << 32);
 #define BEVPOOL_GATHER(V, NARROW, LD)                                                          \
-  hipLaunchKernelGGL((gather_rows_kernel<V, NARROW>), dim3(grid), dim3(kThreads), 0, s,        \
-                     static_cast<const V *>(scratch), vpr, rank, n_points,                    \
-                     static_cast<V *>(x_grad), LD)
+  hipLaunchKernelGGL((gather_rows_kernel<V, NARROW>), dim3(grid + unsigned(warm_blocks)),      \
+                     dim3(kThreads), 0, s, static_cast<const V *>(scratch), vpr, rank,        \
+                     n_points, static_cast<V *>(x_grad), LD, warm_blocks, w, cell_start,     \
+                     cell_end, n_cells, 0)
   if (vec16) {
     const int64_t ld = int64_t(size_t(x_grad_row_stride) * es / 16);
     if (narrow) BEVPOOL_GATHER(u32x4, true, ld); else BEVPOOL_GATHER(u32x4, false, ld);
