@@ -251,11 +251,32 @@ struct BF16 {
 // kept iff 0 <= q_k < nx[k].  In fp32, trunc(q) in [0, n) <=> q > -1 && q < n
 // (NaN fails both), which avoids converting out-of-range floats.
 // Rank: ops/bev_pool/src/bev_pool_triton.py:34-39 with (D, H, W) = (nz, nx, ny).
+__device__ __forceinline__ int quantize_point(float gx, float gy, float gz, uint32_t p,
+                                              uint32_t ppb, float o0, float o1, float o2,
+                                              float d0, float d1, float d2, int n0, int n1,
+                                              int n2) {
+  const float q0 = (gx - o0) / d0;
+  const float q1 = (gy - o1) / d1;
+  const float q2 = (gz - o2) / d2;
+  const bool kept = (q0 > -1.0f) & (q0 < float(n0)) & (q1 > -1.0f) & (q1 < float(n1)) &
+                    (q2 > -1.0f) & (q2 < float(n2));
+  if (!kept) return -1;
+  const int x = int(q0), y = int(q1), z = int(q2);
+  const int b = int(p / ppb);
+  return ((b * n2 + z) * n0 + x) * n1 + y;
+}
+
+// Each thread handles groups of 4 consecutive points (group g of the block:
+// points base + 4 * (g * kThreads + tid) + 0..3); with kVec (row stride 3
+// floats, 16-byte aligned base) a group is three 16-byte loads and one
+// 16-byte rank store.  All groups' loads are issued before any is used.
+template <bool kVec>
 __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
     const float *__restrict__ geom, int64_t n_points, int64_t gstride, int64_t ppb, float o0,
     float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
     int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits,
     int32_t *__restrict__ meta) {
+  constexpr int kGroups = kItems / 4;
   __shared__ int cnt[kMaxRadix];
   if (blockIdx.x == 0 && threadIdx.x < BEVPOOL_META_LEN)  // nothing else touches meta here
     meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
@@ -263,27 +284,76 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
-  __syncthreads();
-  const int64_t base = int64_t(blockIdx.x) * kSortTile;
-  const float f0 = float(n0), f1 = float(n1), f2 = float(n2);
-#pragma unroll 4
-  for (int k = 0; k < kItems; ++k) {
-    const int64_t p = base + int64_t(k) * kThreads + threadIdx.x;
-    if (p < n_points) {
-      const float *g = geom + p * gstride;
-      const float q0 = (g[0] - o0) / d0;
-      const float q1 = (g[1] - o1) / d1;
-      const float q2 = (g[2] - o2) / d2;
-      const bool kept = (q0 > -1.0f) & (q0 < f0) & (q1 > -1.0f) & (q1 < f1) & (q2 > -1.0f) &
-                        (q2 < f2);
-      int r = -1;
-      if (kept) {
-        const int x = int(q0), y = int(q1), z = int(q2);
-        const int b = int(p / ppb);
-        r = ((b * n2 + z) * n0 + x) * n1 + y;
-        atomicAdd(&cnt[unsigned(r) & mask], 1);
+  const uint32_t base = uint32_t(blockIdx.x) * kSortTile;  // n_points < 2^31
+  const uint32_t n = uint32_t(n_points), uppb = uint32_t(ppb);
+  // raw fp32 bits: lanes of a 16-byte load are never bit cast to float
+  // while still in vector form (hipcc 7.2 folded such casts of lanes y/z/w
+  // into lane x)
+  uint32_t g[kGroups][12];
+  const uint32_t *gb = reinterpret_cast<const uint32_t *>(geom);
+#pragma unroll
+  for (int k = 0; k < kGroups; ++k) {
+    const uint32_t p0 = base + 4u * (uint32_t(k) * kThreads + threadIdx.x);
+    if (kVec) {
+      // groups past the last whole one read that one (in bounds, n >= 4);
+      // a partial group is reloaded point by point below
+      const uint32_t last = (n - 4) & ~3u;
+      const uint32_t q0 = p0 + 3 < n ? p0 : last;
+      const u32x4 *src = reinterpret_cast<const u32x4 *>(gb + int64_t(q0) * 3);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const u32x4 v = src[j];
+        g[k][4 * j + 0] = v.x;
+        g[k][4 * j + 1] = v.y;
+        g[k][4 * j + 2] = v.z;
+        g[k][4 * j + 3] = v.w;
       }
-      rank[p] = r;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t p = p0 + u < n ? p0 + u : n - 1;
+        const uint32_t *gp = gb + int64_t(p) * gstride;
+        g[k][3 * u + 0] = gp[0];
+        g[k][3 * u + 1] = gp[1];
+        g[k][3 * u + 2] = gp[2];
+      }
+    }
+  }
+  __syncthreads();  // cnt zeroed
+#pragma unroll
+  for (int k = 0; k < kGroups; ++k) {
+    const uint32_t p0 = base + 4u * (uint32_t(k) * kThreads + threadIdx.x);
+    if (kVec && p0 < n && p0 + 3 >= n) {
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        if (p0 + u < n) {
+          const uint32_t *gp = gb + int64_t(p0 + u) * 3;
+          g[k][3 * u + 0] = gp[0];
+          g[k][3 * u + 1] = gp[1];
+          g[k][3 * u + 2] = gp[2];
+        }
+      }
+    }
+    int r[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      r[u] = quantize_point(__builtin_bit_cast(float, g[k][3 * u]),
+                            __builtin_bit_cast(float, g[k][3 * u + 1]),
+                            __builtin_bit_cast(float, g[k][3 * u + 2]), p0 + u, uppb, o0, o1, o2,
+                            d0, d1, d2, n0, n1, n2);
+      if (r[u] >= 0 && p0 + u < n) atomicAdd(&cnt[unsigned(r[u]) & mask], 1);
+    }
+    if (kVec && p0 + 3 < n) {
+      u32x4 w;
+      w.x = uint32_t(r[0]);
+      w.y = uint32_t(r[1]);
+      w.z = uint32_t(r[2]);
+      w.w = uint32_t(r[3]);
+      *reinterpret_cast<u32x4 *>(rank + p0) = w;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (p0 + u < n) rank[p0 + u] = r[u];
     }
   }
   __syncthreads();
@@ -409,6 +479,24 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
   const int64_t blk0 = int64_t(blockIdx.x) * kSortTile;
   if (blk0 >= n) return;  // whole block leaves before any barrier
 
+  // this wave's keys, in order (loads issued first so that their latency
+  // overlaps the digit-base computation below)
+  uint64_t key[kItems];
+  bool valid[kItems];
+  const int64_t wbase = blk0 + int64_t(w) * kWaveItems;
+#pragma unroll
+  for (int k = 0; k < kItems; ++k) {
+    const int64_t e = wbase + k * 64 + lane;
+    if (kFromRank) {
+      const int r = rank_in[e < n ? e : n - 1];
+      valid[k] = e < n && r >= 0;
+      key[k] = (uint64_t(uint32_t(r)) << 32) | uint64_t(uint32_t(e));
+    } else {
+      valid[k] = e < n;
+      key[k] = keys_in[e < n ? e : n - 1];
+    }
+  }
+
   // digit bases: exclusive scan of the digit totals + this block's prefix
   constexpr int kPer = kMaxRadix / kThreads;  // digits per thread (4)
   int loc[kPer], tsum = 0;
@@ -418,6 +506,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
     loc[i] = d < R ? totals[d] : 0;
     tsum += loc[i];
   }
+  for (int d = tid; d < kWaves * R; d += kThreads) s_cnt[d] = 0;
   int total;
   int ex = block_exclusive_scan(tsum, s_scan, &total);
 #pragma unroll
@@ -427,27 +516,13 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
     ex += loc[i];
   }
   if (kFromRank && blockIdx.x == 0 && tid == 0) meta[BEVPOOL_META_N_KEPT] = total;
-  for (int d = tid; d < kWaves * R; d += kThreads) s_cnt[d] = 0;
   __syncthreads();
 
-  // this wave's keys, in order; per-wave digit counts
-  uint64_t key[kItems];
-  bool valid[kItems];
-  const int64_t wbase = blk0 + int64_t(w) * kWaveItems;
+  // per-wave digit counts
   int *cnt = s_cnt + w * R;
 #pragma unroll
-  for (int k = 0; k < kItems; ++k) {
-    const int64_t e = wbase + k * 64 + lane;
-    if (kFromRank) {
-      const int r = e < n ? rank_in[e] : -1;
-      valid[k] = r >= 0;
-      key[k] = (uint64_t(uint32_t(r)) << 32) | uint64_t(uint32_t(e));
-    } else {
-      valid[k] = e < n;
-      key[k] = valid[k] ? keys_in[e] : 0;
-    }
+  for (int k = 0; k < kItems; ++k)
     if (valid[k]) atomicAdd(&cnt[key_digit(key[k], shift, mask)], 1);
-  }
   __syncthreads();
   for (int d = tid; d < R; d += kThreads) {
     int run = s_base[d];
@@ -480,16 +555,38 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 }
 
 // bev_pool_legacy.py:56-61 boundary flags on the sorted ranks: writes the
-// dense [start, end) of every occupied cell.
+// dense [start, end) of every occupied cell.  Thread t handles sorted
+// positions 4t .. 4t+3 (two 16-byte loads when kVec: keys 16-byte aligned).
+template <bool kVec>
 __global__ __launch_bounds__(kThreads) void cell_ranges_kernel(
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
     int32_t *__restrict__ cstart, int32_t *__restrict__ cend) {
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
-  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (i >= n) return;
-  const int r = key_rank(keys[i]);
-  if (i == 0 || key_rank(keys[i - 1]) != r) cstart[r] = int(i);
-  if (i + 1 == n || key_rank(keys[i + 1]) != r) cend[r] = int(i + 1);
+  const int64_t i0 = (int64_t(blockIdx.x) * kThreads + threadIdx.x) * 4;
+  if (i0 >= n) return;
+  const uint32_t *kw = reinterpret_cast<const uint32_t *>(keys);  // rank = odd words
+  int r[6];  // ranks of positions i0-1 .. i0+4 (-1 outside [0, n))
+  r[0] = i0 > 0 ? int(kw[2 * (i0 - 1) + 1]) : -1;
+  if (kVec && i0 + 3 < n) {
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(kw + 2 * i0);
+    const u32x4 b = *reinterpret_cast<const u32x4 *>(kw + 2 * i0 + 4);
+    r[1] = int(a.y);
+    r[2] = int(a.w);
+    r[3] = int(b.y);
+    r[4] = int(b.w);
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r[1 + u] = i0 + u < n ? int(kw[2 * (i0 + u) + 1]) : -1;
+  }
+  r[5] = i0 + 4 < n ? int(kw[2 * (i0 + 4) + 1]) : -1;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = i0 + u;
+    if (i < n) {
+      if (r[u] != r[u + 1]) cstart[r[u + 1]] = int(i);
+      if (r[u + 2] != r[u + 1]) cend[r[u + 1]] = int(i + 1);
+    }
+  }
 }
 
 // Interval starts (r[i] != r[i-1]) per block of 256 sorted keys: wave ballot
@@ -1477,10 +1574,16 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
     // also resets meta (block 0); an empty input still launches that block
     LaunchTimer t("quantize_geom", s);
     const unsigned grid = L.sort_blocks > 0 ? unsigned(L.sort_blocks) : 1u;
-    hipLaunchKernelGGL(quantize_geom_kernel, dim3(grid), dim3(kThreads), 0, s, geom, n_points,
-                       geom_row_stride, points_per_batch, offset[0], offset[1], offset[2], dx[0],
-                       dx[1], dx[2], nx[0], nx[1], nx[2], rank, at<int32_t>(workspace, L.hist),
-                       int(L.sort_blocks), plan.bits[0], meta);
+    const bool vec = geom_row_stride == 3 && n_points >= 4 &&
+                     reinterpret_cast<uintptr_t>(geom) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(rank) % 16 == 0;
+#define BEVPOOL_QUANT(V)                                                                       \
+  hipLaunchKernelGGL(quantize_geom_kernel<V>, dim3(grid), dim3(kThreads), 0, s, geom, n_points, \
+                     geom_row_stride, points_per_batch, offset[0], offset[1], offset[2], dx[0],  \
+                     dx[1], dx[2], nx[0], nx[1], nx[2], rank, at<int32_t>(workspace, L.hist),   \
+                     int(L.sort_blocks), plan.bits[0], meta)
+    if (vec) BEVPOOL_QUANT(true); else BEVPOOL_QUANT(false);
+#undef BEVPOOL_QUANT
   }
   return check_launch("quantize_geom");
 }
@@ -1577,8 +1680,13 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
   }
   {
     LaunchTimer t("cell_ranges", s);
-    hipLaunchKernelGGL(cell_ranges_kernel, dim3(unsigned(L.cell_blocks)), dim3(kThreads), 0, s,
-                       keys, meta, cell_start, cell_end);
+    const unsigned g = unsigned(ceil_div(n_points, int64_t(kThreads) * 4));
+    if (reinterpret_cast<uintptr_t>(keys) % 16 == 0)
+      hipLaunchKernelGGL(cell_ranges_kernel<true>, dim3(g), dim3(kThreads), 0, s, keys, meta,
+                         cell_start, cell_end);
+    else
+      hipLaunchKernelGGL(cell_ranges_kernel<false>, dim3(g), dim3(kThreads), 0, s, keys, meta,
+                         cell_start, cell_end);
   }
   return check_launch("cell_ranges");
 }
