@@ -272,6 +272,10 @@ def main():
     c_bwd = statistics.median(e[1].elapsed_time(e[2]) for e in cold)
     c_step = statistics.median(e[0].elapsed_time(e[2]) for e in cold)
 
+    # secondary op-level figure: bev_pool(feats (N_kept, C), coords (N_kept, 4))
+    # on the kept points of the same geometry (ops/bev_pool/__init__.py entry)
+    op = op_level(pkg, geom, x.detach(), module, dev)
+
     # per-kernel durations from HIP events on the launch stream
     log(f'[bench] per-kernel timing over {args.profile_steps} steps')
     _lib.timing_reset()
@@ -362,6 +366,7 @@ def main():
             'alg_bytes_per_launch': dom_bytes,
             'avg_us': dom_us,
         },
+        'op_level': op,
         'kernels': kernels,
         'calibration': cal,
     }
@@ -371,10 +376,51 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def op_level(pkg, geom, x, module, dev):
+    """Op-level bev_pool(feats, coords, B, D, H, W) on the kept points (feats
+    (N_kept, C) contiguous, coords int32 (x, y, z, b)): median fwd / bwd over
+    20 back-to-back steps, HIP events; check_bounds off (no host sync)."""
+    B = geom.shape[0]
+    off, d, nx = module.grid()
+    q = ((geom.reshape(B, -1, 3) - torch.tensor(off, device=dev)) /
+         torch.tensor(d, device=dev))
+    n = torch.tensor(nx, device=dev, dtype=torch.float32)
+    kept = ((q > -1) & (q < n)).all(-1)
+    b = torch.arange(B, device=dev).view(B, 1).expand(kept.shape)
+    coords = torch.cat((q.long(), b.unsqueeze(-1)), -1)[kept].to(torch.int32).contiguous()
+    C = x.shape[-1]
+    feats = x.reshape(B, -1, C)[kept].contiguous().requires_grad_(True)
+    X, Y, Z = (int(v) for v in nx)
+    g = torch.randn((B, C, Z, X, Y), device=dev)
+
+    def step():
+        out = pkg.bev_pool(feats, coords, B, Z, X, Y, check_bounds=False)
+        torch.autograd.grad(out, feats, g)
+
+    for _ in range(3):
+        step()
+    evs = []
+    for _ in range(20):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        out = pkg.bev_pool(feats, coords, B, Z, X, Y, check_bounds=False)
+        e[1].record()
+        torch.autograd.grad(out, feats, g)
+        e[2].record()
+        evs.append(e)
+    torch.cuda.synchronize()
+    fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+    bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+    return {'what': 'bev_pool(feats (N_kept, C), coords int32) fwd + autograd bwd, median of 20',
+            'n_points': int(feats.shape[0]), 'fwd_us': round(fwd * 1e3, 1),
+            'bwd_us': round(bwd * 1e3, 1),
+            'points_per_s': round(feats.shape[0] / ((fwd + bwd) * 1e-3), 1)}
+
+
 def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
     """The reference's CPU fallback, restated in torch (oracle/torch_fallback):
     quantise -> kept mask -> compaction -> index_add_ -> permute -> Z-collapse,
-    backward by autograd; same inputs as the GPU run.  Median of 3 after one
+    backward by autograd; same inputs as the GPU run.  Median of 5 after one
     warm-up at the box's thread share, plus one single-thread run."""
     sys.path.insert(0, str(ROOT))
     from oracle import torch_fallback as ref
@@ -395,7 +441,7 @@ def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
     torch.set_num_threads(threads)
     log(f'[bench] cpu baseline, {threads} threads')
     one()
-    runs = [one() for _ in range(3)]
+    runs = [one() for _ in range(5)]
     fwd = statistics.median(r[0] for r in runs)
     bwd = statistics.median(r[1] for r in runs)
     torch.set_num_threads(1)
@@ -416,7 +462,7 @@ def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
         'cores': threads,
         'kind': 'port',
         'sample': f'full det workload ({n_all} points, C=80): torch-CPU restatement of the '
-                  f'reference fallback, fwd+bwd, median of 3 after 1 warm-up',
+                  f'reference fallback, fwd+bwd, median of 5 after 1 warm-up',
         'fwd_ms': round(fwd * 1e3, 2),
         'bwd_ms': round(bwd * 1e3, 2),
         'single_thread': {'value': round(n_all / (f1 + b1), 1), 'fwd_ms': round(f1 * 1e3, 1),

@@ -56,7 +56,7 @@ namespace {
 constexpr int kThreads = 256;              // threads per block, every kernel
 constexpr int kWaves = kThreads / 64;      // wave64 waves per block
 #ifndef BEVPOOL_SORT_ITEMS
-#define BEVPOOL_SORT_ITEMS 16
+#define BEVPOOL_SORT_ITEMS 8
 #endif
 constexpr int kItems = BEVPOOL_SORT_ITEMS;    // keys per thread in sort kernels
 constexpr int kSortTile = kThreads * kItems;  // keys per sort block
@@ -73,7 +73,7 @@ constexpr int kTileChannels = 128;         // max channels per transpose pass
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #ifndef BEVPOOL_RANGE_POINTS
-#define BEVPOOL_RANGE_POINTS 512
+#define BEVPOOL_RANGE_POINTS 256
 #endif
 constexpr int64_t kRangePoints = BEVPOOL_RANGE_POINTS;  // nominal sorted points per forward range
 #ifndef BEVPOOL_XCD_MAP
