@@ -476,8 +476,12 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
   const unsigned mask = unsigned(R - 1);
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const int64_t n = kFromRank ? n_points : int64_t(meta[BEVPOOL_META_N_KEPT]);
-  const int64_t blk0 = int64_t(blockIdx.x) * kSortTile;
-  if (blk0 >= n) return;  // whole block leaves before any barrier
+  // XCD-contiguous tiles: a digit's runs from neighbouring tiles are adjacent
+  // in the output, so writing them from one XCD lets its L2 merge them into
+  // whole lines
+  const int tile = int(xcd_chunk(blockIdx.x, gridDim.x));
+  const int64_t blk0 = int64_t(tile) * kSortTile;
+  if (tile >= nblocks || blk0 >= n) return;  // whole block leaves before any barrier
 
   // this wave's keys, in order (loads issued first so that their latency
   // overlaps the digit-base computation below)
@@ -512,10 +516,10 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int d = tid * kPer + i;
-    if (d < R) s_base[d] = ex + hist[int64_t(d) * nblocks + blockIdx.x];
+    if (d < R) s_base[d] = ex + hist[int64_t(d) * nblocks + tile];
     ex += loc[i];
   }
-  if (kFromRank && blockIdx.x == 0 && tid == 0) meta[BEVPOOL_META_N_KEPT] = total;
+  if (kFromRank && tile == 0 && tid == 0) meta[BEVPOOL_META_N_KEPT] = total;
   __syncthreads();
 
   // per-wave digit counts
@@ -1666,11 +1670,11 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
     {
       LaunchTimer t("radix_scatter", s);
       if (pass == 0) {
-        hipLaunchKernelGGL(radix_scatter_kernel<true>, dim3(nb), dim3(kThreads), 0, s, rank,
+        hipLaunchKernelGGL(radix_scatter_kernel<true>, dim3(xcd_grid(nb)), dim3(kThreads), 0, s, rank,
                            nullptr, n_points, meta, dst, hist, totals, nb, plan.shift[pass],
                            plan.bits[pass]);
       } else {
-        hipLaunchKernelGGL(radix_scatter_kernel<false>, dim3(nb), dim3(kThreads), 0, s, nullptr,
+        hipLaunchKernelGGL(radix_scatter_kernel<false>, dim3(xcd_grid(nb)), dim3(kThreads), 0, s, nullptr,
                            src, n_points, meta, dst, hist, totals, nb, plan.shift[pass],
                            plan.bits[pass]);
       }
