@@ -42,6 +42,7 @@
 #include <stdio.h>
 
 #include <mutex>
+#include <type_traits>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -1097,9 +1098,15 @@ __device__ __forceinline__ bool load_tile_cells(int64_t cell0, int64_t n_cells,
 
 // acc rows (cell-major fp32, written for occupied cells only) -> out
 // (channel-first, dtype T); empty cells are written as 0.  The tile holds the
-// raw fp32 bits: only occupied rows are staged, and a staged 16-byte piece is
-// never converted lane by lane to float (hipcc 7.2 with packed fp32 ops
-// disabled folded bit casts of lanes y/z/w of such a vector into lane x).
+// raw fp32 bits, and a staged 16-byte piece is never converted lane by lane
+// to float (hipcc 7.2 with packed fp32 ops disabled folded bit casts of lanes
+// y/z/w of such a vector into lane x).  With kVecRow every row piece of the
+// tile is loaded up front (kTileSlots per thread, clamped in-bounds
+// addresses, empty cells included) together with the occupancy loads, so a
+// block pays one memory latency before its stores.  Occupancy: cell_end != 0
+// (cell ranges are zeroed before the sort writes the occupied ones).
+constexpr int kTileSlots = kCellTile * (kTileChannels / 4) / kThreads;  // 8
+
 template <typename T, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
     const float *__restrict__ acc, int C, int CT, const int32_t *__restrict__ cstart,
@@ -1109,32 +1116,57 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
   extern __shared__ uint32_t tile_bits[];  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
   __shared__ int64_t off[kCellTile];
+  (void)cstart;
   const int tid = threadIdx.x;
   const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
-  const bool any = load_tile_cells(cell0, n_cells, cstart, cend, n_z, n_xy, sb, sz, occ, off);
+  int occ_mine = 0;
+  int64_t off_mine = -1;
+  if (tid < kCellTile && cell0 + tid < n_cells) {
+    occ_mine = cend[cell0 + tid] != 0 ? 1 : 0;
+    off_mine = cell_offset(uint32_t(cell0 + tid), uint32_t(n_z), uint32_t(n_xy), sb, sz);
+  }
   const uint32_t *accb = reinterpret_cast<const uint32_t *>(acc);
   const int pitch = CT + 1;
+  if (!kVecRow) {
+    if (tid < kCellTile) {
+      occ[tid] = occ_mine;
+      off[tid] = off_mine;
+    }
+    __syncthreads();
+  }
   for (int c0 = 0; c0 < C; c0 += CT) {
     const int cb = C - c0 < CT ? C - c0 : CT;
-    if (any) {
-      if (kVecRow) {
-        const uint32_t q = uint32_t(cb) >> 2;  // 16-byte pieces per row
-        for (uint32_t i = tid; i < kCellTile * q; i += kThreads) {
+    if (kVecRow) {
+      const uint32_t q = uint32_t(cb) >> 2;  // 16-byte pieces per row
+      const uint32_t n_items = kCellTile * q;
+      u32x4 v[kTileSlots];
+#pragma unroll
+      for (int it = 0; it < kTileSlots; ++it) {
+        const uint32_t i = tid + it * kThreads;
+        uint32_t t = i / q, k = i - t * q;
+        if (i >= n_items || cell0 + t >= n_cells) t = k = 0;
+        v[it] = *reinterpret_cast<const u32x4 *>(accb + (cell0 + t) * C + c0 + 4 * k);
+      }
+      if (c0 == 0 && tid < kCellTile) {
+        occ[tid] = occ_mine;
+        off[tid] = off_mine;
+      }
+#pragma unroll
+      for (int it = 0; it < kTileSlots; ++it) {
+        const uint32_t i = tid + it * kThreads;
+        if (i < n_items) {
           const uint32_t t = i / q, k = i - t * q;
-          if (occ[t]) {
-            const u32x4 v = *reinterpret_cast<const u32x4 *>(accb + (cell0 + t) * C + c0 + 4 * k);
-            uint32_t *d = tile_bits + t * pitch + 4 * k;
-            d[0] = v.x;
-            d[1] = v.y;
-            d[2] = v.z;
-            d[3] = v.w;
-          }
+          uint32_t *d = tile_bits + t * pitch + 4 * k;
+          d[0] = v[it].x;
+          d[1] = v[it].y;
+          d[2] = v[it].z;
+          d[3] = v[it].w;
         }
-      } else {
-        for (uint32_t i = tid; i < uint32_t(kCellTile * cb); i += kThreads) {
-          const uint32_t t = i / uint32_t(cb), c = i - t * uint32_t(cb);
-          if (occ[t]) tile_bits[t * pitch + c] = accb[(cell0 + t) * C + c0 + c];
-        }
+      }
+    } else {
+      for (uint32_t i = tid; i < uint32_t(kCellTile * cb); i += kThreads) {
+        const uint32_t t = i / uint32_t(cb), c = i - t * uint32_t(cb);
+        if (occ[t]) tile_bits[t * pitch + c] = accb[(cell0 + t) * C + c0 + c];
       }
     }
     __syncthreads();
@@ -1143,7 +1175,7 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
       raw r[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t b = (any && occ[j + u]) ? tile_bits[(j + u) * pitch + c] : 0u;
+        const uint32_t b = occ[j + u] ? tile_bits[(j + u) * pitch + c] : 0u;
         r[u] = T::to_raw(__builtin_bit_cast(float, b));
       }
       if (kVecBev) {
@@ -1177,8 +1209,10 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
 // ---------------------------------------------------------------------------
 
 // grad (channel-first, any b/c/z strides, xy contiguous) -> cell-major rows of
-// the occupied cells (raw bits copied); tiles without an occupied cell exit.
-//
+// the occupied cells (raw bits copied).  With kVecBev each thread always
+// handles the same 4 cells (j = 4 * (tid % 16)) of channels tid / 16 + 16 it;
+// all its tile loads are issued up front (clamped in-bounds addresses,
+// empty cells included) together with the occupancy loads.
 template <typename TR, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
     const TR *__restrict__ grad, int C, int CT, const int32_t *__restrict__ cstart,
@@ -1190,41 +1224,91 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
   __shared__ int64_t off[kCellTile];
   const int tid = threadIdx.x;
   const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
-  if (!load_tile_cells(cell0, n_cells, cstart, cend, n_z, n_xy, sb, sz, occ, off)) return;
   const int pitch = CT + 1;
   constexpr int kPer = 16 / int(sizeof(TR));  // elements per 16-byte row piece
+  if (kVecBev) {
+    (void)cstart;
+    int occ_mine = 0;
+    if (tid < kCellTile && cell0 + tid < n_cells) occ_mine = cend[cell0 + tid] != 0 ? 1 : 0;
+    const int j = (tid & 15) * 4;
+    const bool live = cell0 + j < n_cells;  // then all 4 cells are (n_cells % 4 == 0)
+    const int64_t offj =
+        cell_offset(uint32_t(live ? cell0 + j : cell0), uint32_t(n_z), uint32_t(n_xy), sb, sz);
+    for (int c0 = 0; c0 < C; c0 += CT) {
+      const int cb = C - c0 < CT ? C - c0 : CT;
+      using V = typename std::conditional<sizeof(TR) == 4, u32x4, u32x2>::type;
+      V v[kTileSlots];
+#pragma unroll
+      for (int it = 0; it < kTileSlots; ++it) {
+        int c = (tid >> 4) + 16 * it;
+        c = c < cb ? c : 0;
+        v[it] = *reinterpret_cast<const V *>(grad + offj + int64_t(c0 + c) * sc);
+      }
+      if (c0 == 0 && tid < kCellTile) occ[tid] = occ_mine;
+#pragma unroll
+      for (int it = 0; it < kTileSlots; ++it) {
+        const int c = (tid >> 4) + 16 * it;
+        if (c < cb) {
+          TR e[4];
+          if constexpr (sizeof(TR) == 4) {
+            e[0] = v[it].x;
+            e[1] = v[it].y;
+            e[2] = v[it].z;
+            e[3] = v[it].w;
+          } else {
+            e[0] = TR(v[it].x);
+            e[1] = TR(v[it].x >> 16);
+            e[2] = TR(v[it].y);
+            e[3] = TR(v[it].y >> 16);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) tile[(j + u) * pitch + c] = e[u];
+        }
+      }
+      __syncthreads();
+      if (kVecRow) {
+        const uint32_t q = uint32_t(cb) / kPer;  // 16-byte pieces per row
+        for (uint32_t i = tid; i < kCellTile * q; i += kThreads) {
+          const uint32_t t = i / q, k = i - t * q;
+          if (!occ[t]) continue;
+          const TR *srow = tile + t * pitch + kPer * k;
+          u32x4 w;
+          if constexpr (sizeof(TR) == 4) {
+            w.x = srow[0];
+            w.y = srow[1];
+            w.z = srow[2];
+            w.w = srow[3];
+          } else {
+            w.x = uint32_t(srow[0]) | (uint32_t(srow[1]) << 16);
+            w.y = uint32_t(srow[2]) | (uint32_t(srow[3]) << 16);
+            w.z = uint32_t(srow[4]) | (uint32_t(srow[5]) << 16);
+            w.w = uint32_t(srow[6]) | (uint32_t(srow[7]) << 16);
+          }
+          *reinterpret_cast<u32x4 *>(rows + (cell0 + t) * C + c0 + kPer * k) = w;
+        }
+      } else {
+        for (uint32_t i = tid; i < uint32_t(kCellTile * cb); i += kThreads) {
+          const uint32_t t = i / uint32_t(cb), c = i - t * uint32_t(cb);
+          if (occ[t]) rows[(cell0 + t) * C + c0 + c] = tile[t * pitch + c];
+        }
+      }
+      __syncthreads();
+    }
+    return;
+  }
+  // general strides: per-cell loads after the occupancy test
+  if (!load_tile_cells(cell0, n_cells, cstart, cend, n_z, n_xy, sb, sz, occ, off)) return;
   for (int c0 = 0; c0 < C; c0 += CT) {
     const int cb = C - c0 < CT ? C - c0 : CT;
     for (int i = tid; i < cb * (kCellTile / 4); i += kThreads) {
       const int c = i >> 4, j = (i & 15) * 4;
-      if (!(occ[j] | occ[j + 1] | occ[j + 2] | occ[j + 3])) continue;
-      TR v[4];
-      if (kVecBev) {
-        const TR *src = grad + off[j] + int64_t(c0 + c) * sc;
-        if constexpr (sizeof(TR) == 4) {
-          const u32x4 w = *reinterpret_cast<const u32x4 *>(src);
-          v[0] = w.x;
-          v[1] = w.y;
-          v[2] = w.z;
-          v[3] = w.w;
-        } else {
-          const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
-          v[0] = TR(w.x);
-          v[1] = TR(w.x >> 16);
-          v[2] = TR(w.y);
-          v[3] = TR(w.y >> 16);
-        }
-      } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          v[u] = occ[j + u] ? grad[off[j + u] + int64_t(c0 + c) * sc] : TR(0);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) tile[(j + u) * pitch + c] = v[u];
+      for (int u = 0; u < 4; ++u)
+        tile[(j + u) * pitch + c] = occ[j + u] ? grad[off[j + u] + int64_t(c0 + c) * sc] : TR(0);
     }
     __syncthreads();
     if (kVecRow) {
-      const uint32_t q = uint32_t(cb) / kPer;  // 16-byte pieces per row
+      const uint32_t q = uint32_t(cb) / kPer;
       for (uint32_t i = tid; i < kCellTile * q; i += kThreads) {
         const uint32_t t = i / q, k = i - t * q;
         if (!occ[t]) continue;
