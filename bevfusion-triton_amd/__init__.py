@@ -7,6 +7,8 @@ ziyangyeh/bevfusion-triton behind the reference's own Python surface:
   BevPoolFunction                           ops/bev_pool/src/bev_pool_triton.py:153-216
   gen_dx_bx / BevPoolTransform.bev_pool     models/vtransforms/base.py:19-23, 131-165
   lss_bev_pool                              the same as a function
+  lss_bev_pool_depth                        the same fused with depth_lss.py:91-94's
+                                            depth (x) context product
 
 The kernels live in ``csrc/bevpool.hip`` and are reached through the C ABI of
 ``include/bevpool.h`` (``libbevpool_amd.so``, loaded by ``_lib``).  There is no
@@ -17,7 +19,8 @@ The directory name is not a Python identifier; load it with
 """
 from ._lib import BevPoolError, LibraryNotBuilt, library
 from .bev_pool import BevPoolFunction, BevPoolIndexExport, bev_pool
-from .vtransform import BevPoolTransform, LSSIndexExport, gen_dx_bx, host_grid, lss_bev_pool
+from .vtransform import (BevPoolTransform, LSSIndexExport, gen_dx_bx, host_grid, lss_bev_pool,
+                         lss_bev_pool_depth)
 
 __all__ = [
     'BevPoolError',
@@ -31,4 +34,5 @@ __all__ = [
     'host_grid',
     'library',
     'lss_bev_pool',
+    'lss_bev_pool_depth',
 ]

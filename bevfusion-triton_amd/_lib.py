@@ -67,6 +67,17 @@ _SIGNATURES = {
          _vp, _sz, _vp],
         ctypes.c_int,
     ),
+    'bevpool_context_rows': ([_vp, _i64, _i64, _i32, _i32, _i64, _vp, _vp], ctypes.c_int),
+    'bevpool_forward_depth': (
+        [_vp, _vp, _i32, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64,
+         _i64, _vp, _vp, _sz, _vp],
+        ctypes.c_int,
+    ),
+    'bevpool_backward_depth': (
+        [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32,
+         _i64, _vp, _vp, _i64, _i64, _vp, _sz, _vp],
+        ctypes.c_int,
+    ),
     'bevpool_timing_enable': ([ctypes.c_int], ctypes.c_int),
     'bevpool_timing_reset': ([], ctypes.c_int),
     'bevpool_timing_read': (

@@ -240,3 +240,60 @@ def _backward_call(lib, idx, grad, dtype, C, stride_b, stride_c, stride_z, x_gra
         ),
         'bevpool_backward',
     )
+
+
+# ---- depth-weighted (fused depth x context) pooling -------------------------
+
+def context_rows(context3d):
+    """(BN, C, HW) fp32 context with HW contiguous -> (BN*HW, C) rows."""
+    BN, C, HW = context3d.shape
+    if context3d.stride(2) != 1:
+        context3d = context3d.contiguous()
+    rows = torch.empty((BN * HW, C), dtype=torch.float32, device=context3d.device)
+    with torch.cuda.device(context3d.device):
+        L.check(
+            L.library().bevpool_context_rows(
+                L.ptr(context3d), context3d.stride(0), context3d.stride(1), BN, C, HW,
+                L.ptr(rows), L.stream_handle(context3d.device),
+            ),
+            'bevpool_context_rows',
+        )
+    return rows
+
+
+def forward_depth(idx: PoolIndex, depth_flat, rows, D: int, HW: int, out, stride_b: int,
+                  stride_c: int, stride_z: int) -> None:
+    """Pool depth[p] * rows[pix(p)] into `out` (fp32, strides as forward)."""
+    C = rows.shape[1]
+    lib = L.library()
+    scratch_bytes = lib.bevpool_forward_scratch_bytes(idx.n_cells, C)
+    scratch = torch.empty(max(int(scratch_bytes), 256), dtype=torch.uint8, device=idx.device)
+    with torch.cuda.device(idx.device):
+        L.check(
+            lib.bevpool_forward_depth(
+                L.ptr(depth_flat), L.ptr(rows), C, idx.n_points, D, HW, L.ptr(idx.keys),
+                L.ptr(idx.cell_start), L.ptr(idx.cell_end), L.ptr(idx.meta), idx.B, idx.D,
+                idx.H * idx.W, stride_b, stride_c, stride_z, L.ptr(out), L.ptr(scratch),
+                scratch.numel(), L.stream_handle(idx.device),
+            ),
+            'bevpool_forward_depth',
+        )
+
+
+def backward_depth(idx: PoolIndex, grad, C: int, stride_b: int, stride_c: int, stride_z: int,
+                   depth_flat, rows, D: int, HW: int, grad_depth, grad_context3d) -> None:
+    """grad_depth (n_points,) and grad_context (BN, C, HW) <- grad."""
+    lib = L.library()
+    scratch_bytes = lib.bevpool_backward_scratch_bytes(idx.n_cells, C, L.F32)
+    scratch = torch.empty(max(int(scratch_bytes), 256), dtype=torch.uint8, device=idx.device)
+    with torch.cuda.device(idx.device):
+        L.check(
+            lib.bevpool_backward_depth(
+                L.ptr(grad), stride_b, stride_c, stride_z, C, L.ptr(idx.rank), idx.n_points, D,
+                HW, L.ptr(depth_flat), L.ptr(rows), L.ptr(idx.cell_start), L.ptr(idx.cell_end),
+                idx.B, idx.D, idx.H * idx.W, L.ptr(grad_depth), L.ptr(grad_context3d),
+                grad_context3d.stride(0), grad_context3d.stride(1), L.ptr(scratch),
+                scratch.numel(), L.stream_handle(idx.device),
+            ),
+            'bevpool_backward_depth',
+        )

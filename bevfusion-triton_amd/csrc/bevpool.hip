@@ -23,10 +23,16 @@
 //   backward
 //     bev_to_rows_kernel<T>     channel-first grad tile -> cell-major rows
 //                               (occupied cells only) via LDS transpose
-//     gather_warm_kernel        reads the ranks (per XCD) and the occupied
-//                               rows once so the gather finds them cached
-//     gather_rows_kernel<V>     point-order streaming copy of each point's
-//                               cell row (zero rows for dropped points)
+//     gather_rows_kernel<V>     leading blocks read the ranks (per XCD) and the
+//                               occupied rows once so the rest find them
+//                               cached; then a point-order streaming copy of
+//                               each point's cell row (zero rows for dropped
+//                               points)
+//   depth-weighted pooling (fused depth x context)
+//     context_rows_kernel       context (BN, C, HW) -> channel-last rows
+//     accum_pipe_kernel<..,true> forward sums of depth[p] * ctx[pix(p)]
+//     depth_grad_kernel         grad_depth (dot products) and grad_context
+//                               (depth-weighted sums along each ray)
 //
 // Numerics: the quantisation is IEEE fp32 subtraction followed by a correctly
 // rounded fp32 division (built without fast-math, with
@@ -793,11 +799,26 @@ struct LoaderRing {
   u32x4 d[kDepth][kSlots];       // gathered 16-byte pieces of a stage
   uint32_t idx[kDepth][kSlots];  // point indices of a later stage
   int rk[kDepth];                // rank of row (lt % kStageRows) of a stage
+  uint32_t dpi[kDepth];          // depth-weighted rows: point index of that row
+  float dp[kDepth];              //   and its depth weight
+};
+
+// Rows of the depth-weighted forward (fused depth x context pooling): the row
+// of point p = (bn*D + d)*HW + hw is context row pix = bn*HW + hw, weighted by
+// depth[p] (the reference materialises depth[p] * context[pix, c],
+// models/vtransforms/depth_lss.py:91-94).
+struct DepthRows {
+  const float *depth;  // (BN, D, HW) contiguous: depth[p]
+  uint32_t dhw, hw;    // D*HW, HW
+  __device__ __forceinline__ uint32_t pix(uint32_t p) const {
+    const uint32_t bn = p / dhw;
+    return bn * hw + (p - bn * dhw) % hw;
+  }
 };
 
 // Point indices of stage k into ring slot j.  Slots past the stage's rows
 // repeat its last row; a stage past the range end reads the range's first row.
-template <int kSlots, int j>
+template <int kSlots, int j, bool kMul>
 __device__ __forceinline__ void ring_index(LoaderRing<kSlots> &R, int lt,
                                            const uint32_t *__restrict__ kw, const PipeRange &pr,
                                            int k) {
@@ -809,31 +830,39 @@ __device__ __forceinline__ void ring_index(LoaderRing<kSlots> &R, int lt,
     r = r < rows - 1 ? r : rows - 1;
     R.idx[j][i] = kw[2 * (rows > 0 ? base + r : pr.s)];  // low word: point index
   }
+  if constexpr (kMul) {
+    int64_t p = base + (lt & (kStageRows - 1));
+    p = base >= pr.e ? pr.s : (p < pr.e ? p : pr.e - 1);
+    R.dpi[j] = kw[2 * p];
+  }
 }
 
 // Rows of stage k into ring slot j (its indices are in R.idx[j]), plus the rank
 // of row lt % kStageRows.
-template <int kSlots, int j>
+template <int kSlots, int j, bool kMul>
 __device__ __forceinline__ void ring_rows(LoaderRing<kSlots> &R, int lt,
                                           const uint32_t *__restrict__ kw,
                                           const char *__restrict__ xb, int64_t ld_bytes,
-                                          int col_bytes, const PipeRange &pr, int k) {
+                                          int col_bytes, const PipeRange &pr, int k,
+                                          const DepthRows &dr) {
   const bool live = pr.rows(k) > 0;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
     const int slot = lt + kLoaders * i;
     const int q = live ? slot - (slot / pr.rowq) * pr.rowq : 0;
-    R.d[j][i] = *reinterpret_cast<const u32x4 *>(xb + int64_t(R.idx[j][i]) * ld_bytes +
-                                                 col_bytes + q * 16);
+    const uint32_t row = kMul ? dr.pix(R.idx[j][i]) : R.idx[j][i];
+    R.d[j][i] =
+        *reinterpret_cast<const u32x4 *>(xb + int64_t(row) * ld_bytes + col_bytes + q * 16);
   }
   const int64_t b = pr.s + int64_t(k) * kStageRows;
   int64_t p = b + (lt & (kStageRows - 1));
   p = b >= pr.e ? pr.s : (p < pr.e ? p : pr.e - 1);
   R.rk[j] = kw[2 * p + 1];  // high word: rank
+  if constexpr (kMul) R.dp[j] = dr.depth[R.dpi[j]];
 }
 
 // Ring slot j (stage k) into an LDS buffer.
-template <int kSlots, int j>
+template <int kSlots, int j, bool kMul>
 __device__ __forceinline__ void ring_store(const LoaderRing<kSlots> &R, int lt,
                                            const PipeRange &pr, int k, u32x4 *__restrict__ lbuf,
                                            int *__restrict__ lrk) {
@@ -843,24 +872,29 @@ __device__ __forceinline__ void ring_store(const LoaderRing<kSlots> &R, int lt,
     const int slot = lt + kLoaders * i;
     if (slot < n) lbuf[slot] = R.d[j][i];
   }
-  if (lt < kStageRows) lrk[lt] = R.rk[j];
+  if (lt < kStageRows) {
+    lrk[lt] = R.rk[j];
+    // depth weights follow the ranks (lrk + kStageRows)
+    if constexpr (kMul) lrk[kStageRows + lt] = __builtin_bit_cast(int, R.dp[j]);
+  }
 }
 
 // One loader step k with ring slot r = k % kDepth (a template constant).
-template <int kSlots, int r>
+template <int kSlots, int r, bool kMul>
 __device__ __forceinline__ void loader_step(LoaderRing<kSlots> &R, int lt,
                                             const uint32_t *__restrict__ kw,
                                             const char *__restrict__ xb, int64_t ld_bytes,
                                             int col_bytes, const PipeRange &pr, int k, int nst,
                                             u32x4 *__restrict__ buf0, u32x4 *__restrict__ buf1,
-                                            int *__restrict__ rk0s, int *__restrict__ rk1s) {
-  ring_rows<kSlots, r>(R, lt, kw, xb, ld_bytes, col_bytes, pr, k + kDepth);
-  ring_index<kSlots, r>(R, lt, kw, pr, k + 2 * kDepth);
+                                            int *__restrict__ rk0s, int *__restrict__ rk1s,
+                                            const DepthRows &dr) {
+  ring_rows<kSlots, r, kMul>(R, lt, kw, xb, ld_bytes, col_bytes, pr, k + kDepth, dr);
+  ring_index<kSlots, r, kMul>(R, lt, kw, pr, k + 2 * kDepth);
   if (k + 1 < nst) {
     if ((k + 1) & 1)
-      ring_store<kSlots, (r + 1) % kDepth>(R, lt, pr, k + 1, buf1, rk1s);
+      ring_store<kSlots, (r + 1) % kDepth, kMul>(R, lt, pr, k + 1, buf1, rk1s);
     else
-      ring_store<kSlots, (r + 1) % kDepth>(R, lt, pr, k + 1, buf0, rk0s);
+      ring_store<kSlots, (r + 1) % kDepth, kMul>(R, lt, pr, k + 1, buf0, rk0s);
   }
   __syncthreads();
 }
@@ -907,6 +941,9 @@ struct RowSum {
 
   // lb: the stage's rows in LDS (row stride cb elements), col: this lane's
   // columns; nch: channels of this wave (stores of lanes past nch are skipped).
+  // kMul: each row is first multiplied by its weight (fp32 bits at
+  // lrk[kStageRows + row]); product and sum are separate roundings.
+  template <bool kMul>
   __device__ __forceinline__ void add_stage(const typename T::raw *__restrict__ lb,
                                             const int *__restrict__ lrk, int rows, int cb,
                                             const int (&col)[kCPL], int nch,
@@ -924,6 +961,14 @@ struct RowSum {
       for (int u = 0; u < kB; ++u)
 #pragma unroll
         for (int i = 0; i < kCPL; ++i) v[u][i] = T::load(lb + (j0 + u) * cb + col[i]);
+      if constexpr (kMul) {
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const float wgt = __builtin_bit_cast(float, lrk[kStageRows + j0 + u]);
+#pragma unroll
+          for (int i = 0; i < kCPL; ++i) v[u][i] = v[u][i] * wgt;
+        }
+      }
       const uint32_t chunk = uint32_t(starts >> j0) & uint32_t((uint64_t(1) << kB) - 1);
       const bool full = j0 + kB <= rows;
       if (full && chunk == 0) {
@@ -965,18 +1010,21 @@ struct RowSum {
   }
 };
 
-template <typename T, int kSlots, int kCPL>
+// kMul: depth-weighted rows (DepthRows): xb holds the context rows and row
+// p's values are depth[p] * ctx[pix(p)].
+template <typename T, int kSlots, int kCPL, bool kMul>
 __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
     const char *__restrict__ xb, int64_t ld_bytes, int C, int CB,
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
-    const int32_t *__restrict__ cend, float *__restrict__ acc, int64_t P) {
+    const int32_t *__restrict__ cend, float *__restrict__ acc, int64_t P, DepthRows dr) {
   using raw = typename T::raw;
   extern __shared__ u32x4 smem4[];
   const int rowq_max = CB * int(sizeof(raw)) / 16;
   u32x4 *buf0 = smem4;
   u32x4 *buf1 = smem4 + kStageRows * rowq_max;
+  // per stage buffer: kStageRows ranks, then kStageRows depth weights
   int *rk0s = reinterpret_cast<int *>(smem4 + 2 * kStageRows * rowq_max);
-  int *rk1s = rk0s + kStageRows;
+  int *rk1s = rk0s + 2 * kStageRows;
   const uint32_t *kw = reinterpret_cast<const uint32_t *>(keys);
 
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
@@ -1013,8 +1061,8 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
 #pragma unroll
         for (int r = 0; r < kDepth; ++r) {
           const int kk = k + r;
-          st.add_stage(reinterpret_cast<const raw *>((kk & 1) ? buf1 : buf0),
-                       (kk & 1) ? rk1s : rk0s, pr.rows(kk), cb, col, nch, out, C);
+          st.template add_stage<kMul>(reinterpret_cast<const raw *>((kk & 1) ? buf1 : buf0),
+                                      (kk & 1) ? rk1s : rk0s, pr.rows(kk), cb, col, nch, out, C);
           __syncthreads();
         }
       }
@@ -1025,25 +1073,25 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
       // prologue: indices of stages 0..D-1, rows of 0..D-1 each followed by the
       // indices of stage j+D; then stage 0 into LDS
 #define BEVPOOL_RING_PRO(J)                                                                    \
-  if constexpr ((J) < kDepth) ring_index<kSlots, (J)>(R, lt, kw, pr, (J));
+  if constexpr ((J) < kDepth) ring_index<kSlots, (J), kMul>(R, lt, kw, pr, (J));
       BEVPOOL_RING_PRO(0) BEVPOOL_RING_PRO(1) BEVPOOL_RING_PRO(2) BEVPOOL_RING_PRO(3)
       BEVPOOL_RING_PRO(4) BEVPOOL_RING_PRO(5) BEVPOOL_RING_PRO(6) BEVPOOL_RING_PRO(7)
 #undef BEVPOOL_RING_PRO
 #define BEVPOOL_RING_PRO(J)                                                                    \
   if constexpr ((J) < kDepth) {                                                               \
-    ring_rows<kSlots, (J)>(R, lt, kw, xb, ld_bytes, col_bytes, pr, (J));                      \
-    ring_index<kSlots, (J)>(R, lt, kw, pr, (J) + kDepth);                                     \
+    ring_rows<kSlots, (J), kMul>(R, lt, kw, xb, ld_bytes, col_bytes, pr, (J), dr);            \
+    ring_index<kSlots, (J), kMul>(R, lt, kw, pr, (J) + kDepth);                               \
   }
       BEVPOOL_RING_PRO(0) BEVPOOL_RING_PRO(1) BEVPOOL_RING_PRO(2) BEVPOOL_RING_PRO(3)
       BEVPOOL_RING_PRO(4) BEVPOOL_RING_PRO(5) BEVPOOL_RING_PRO(6) BEVPOOL_RING_PRO(7)
 #undef BEVPOOL_RING_PRO
-      ring_store<kSlots, 0>(R, lt, pr, 0, buf0, rk0s);
+      ring_store<kSlots, 0, kMul>(R, lt, pr, 0, buf0, rk0s);
       __syncthreads();
       for (int k = 0; k < nst; k += kDepth) {
 #define BEVPOOL_RING_STEP(J)                                                                   \
   if constexpr ((J) < kDepth)                                                                 \
-    loader_step<kSlots, (J)>(R, lt, kw, xb, ld_bytes, col_bytes, pr, k + (J), nst, buf0, buf1, \
-                             rk0s, rk1s);
+    loader_step<kSlots, (J), kMul>(R, lt, kw, xb, ld_bytes, col_bytes, pr, k + (J), nst, buf0, \
+                                   buf1, rk0s, rk1s, dr);
         BEVPOOL_RING_STEP(0) BEVPOOL_RING_STEP(1) BEVPOOL_RING_STEP(2) BEVPOOL_RING_STEP(3)
         BEVPOOL_RING_STEP(4) BEVPOOL_RING_STEP(5) BEVPOOL_RING_STEP(6) BEVPOOL_RING_STEP(7)
 #undef BEVPOOL_RING_STEP
@@ -1337,7 +1385,7 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
   }
 }
 
-// Cache warm-up for gather_rows_kernel.  Each gather piece is a dependent
+// Cache warm-up for gather_rows_kernel (its leading blocks).  Each gather piece is a dependent
 // chain rank -> row -> store; with the rank array and the gradient rows
 // fetched from HBM while the gather's write stream saturates it, the chains
 // take about twice as long (measured 92 us vs 155-185 us at the det shape).
@@ -1419,12 +1467,6 @@ __device__ __forceinline__ void gather_warm_block(const GatherWarm &w, int wb, i
   if (never) sink[threadIdx.x] = m;
 }
 
-__global__ __launch_bounds__(kThreads) void gather_warm_kernel(
-    GatherWarm w, int64_t n_points, const int32_t *__restrict__ cstart,
-    const int32_t *__restrict__ cend, int64_t n_cells, int never, uint32_t *__restrict__ sink) {
-  gather_warm_block(w, int(blockIdx.x), n_points, cstart, cend, n_cells, never, sink);
-}
-
 // x_grad[p, :] = rows[rank[p], :] (kept) or 0 (dropped); point order, so the
 // writes stream.  V is a 16-byte vector when rows allow it, else one element.
 // Each thread copies kGatherPer vectors spaced kThreads apart (coalesced),
@@ -1432,17 +1474,14 @@ __global__ __launch_bounds__(kThreads) void gather_warm_kernel(
 // cells, whose rows then stay in its L2), and the destination is written
 // with non-temporal stores (it is not read again here, and keeping it out of
 // L2 leaves room for the gradient rows).  Each piece is a dependent chain
-// rank -> row -> store, so the kernel runs after gather_warm_kernel has
-// pulled the ranks and the rows into the caches.  kNarrow: indices fit in 32
+// rank -> row -> store, so the leading warm_blocks blocks first pull the ranks
+// and the rows into the caches (gather_warm_block).  kNarrow: indices fit in 32
 // bits.
 #ifndef BEVPOOL_GATHER_PER
 #define BEVPOOL_GATHER_PER 1
 #endif
 #ifndef BEVPOOL_GATHER_NT
 #define BEVPOOL_GATHER_NT 1
-#endif
-#ifndef BEVPOOL_SEPARATE_WARM
-#define BEVPOOL_SEPARATE_WARM 0
 #endif
 constexpr int kGatherPer = BEVPOOL_GATHER_PER;
 
@@ -1486,6 +1525,113 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
       xg[p * xg_ld + q] = v;
 #endif
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// depth-weighted (fused depth x context) pooling helpers
+// ---------------------------------------------------------------------------
+
+// context (BN, C, HW), element (bn, c, hw) at bn*sbn + c*sc + hw (hw
+// contiguous), -> rows (BN*HW, C) fp32 channel-last; 64 pixels x up to
+// kTileChannels channels per pass through LDS.
+__global__ __launch_bounds__(kThreads) void context_rows_kernel(
+    const float *__restrict__ ctx, int C, int64_t HW, int64_t n_pix, int64_t sbn, int64_t sc,
+    float *__restrict__ rows) {
+  extern __shared__ float ctile[];  // kCellTile * (CT + 1)
+  const int tid = threadIdx.x;
+  const int64_t pix0 = int64_t(blockIdx.x) * kCellTile;
+  const int CT = C < kTileChannels ? C : kTileChannels;
+  const int pitch = CT + 1;
+  for (int c0 = 0; c0 < C; c0 += CT) {
+    const int cb = C - c0 < CT ? C - c0 : CT;
+    for (int i = tid; i < kCellTile * cb; i += kThreads) {
+      const int c = i / kCellTile, t = i - c * kCellTile;
+      const int64_t pix = pix0 + t;
+      float v = 0.0f;
+      if (pix < n_pix) {
+        const int64_t bn = pix / HW, hw = pix - bn * HW;
+        v = ctx[bn * sbn + int64_t(c0 + c) * sc + hw];
+      }
+      ctile[t * pitch + c] = v;
+    }
+    __syncthreads();
+    for (int i = tid; i < kCellTile * cb; i += kThreads) {
+      const int t = i / cb, c = i - t * cb;
+      if (pix0 + t < n_pix) rows[(pix0 + t) * C + c0 + c] = ctile[t * pitch + c];
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Backward of out[cell] = sum_{p in cell} depth[p] * ctx[pix(p)] (the
+// reference's autograd through depth_lss.py:91-94 and the pooling):
+//   grad_depth[p]        = sum_c g[rank[p], c] * ctx[pix(p), c]  (0 if dropped)
+//   grad_ctx[bn, c, hw]  = sum_d g[rank[p_d], c] * depth[p_d]
+// with p_d = (bn*D + d)*HW + hw.  One wave per pixel; lane l holds channels
+// l + 64 i (i < kCPL); the dot product is a fixed-order butterfly over the
+// wave, the context sum runs over d in order.  g: cell-major fp32 rows of the
+// occupied cells; ctx: channel-last rows (context_rows_kernel).
+template <int kCPL, int kU>
+__global__ __launch_bounds__(kThreads) void depth_grad_kernel(
+    const float *__restrict__ g, int C, const int32_t *__restrict__ rank,
+    const float *__restrict__ depth, const float *__restrict__ ctx, int D, int64_t HW,
+    int64_t n_pix, float *__restrict__ grad_depth, float *__restrict__ grad_ctx,
+    int64_t gsbn, int64_t gsc) {
+  const int lane = lane_id();
+  const int64_t pix = (int64_t(blockIdx.x) * kThreads + threadIdx.x) >> 6;
+  if (pix >= n_pix) return;  // whole wave
+  const int64_t bn = pix / HW, hw = pix - bn * HW;
+  float xc[kCPL], gc[kCPL];
+#pragma unroll
+  for (int i = 0; i < kCPL; ++i) {
+    const int c = lane + 64 * i;
+    xc[i] = c < C ? ctx[pix * C + c] : 0.0f;
+    gc[i] = 0.0f;
+  }
+  const int64_t p0 = bn * int64_t(D) * HW + hw;  // point of depth bin d: p0 + d * HW
+  for (int d0 = 0; d0 < D; d0 += kU) {
+    int r[kU];
+    float dp[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int d = d0 + u < D ? d0 + u : D - 1;
+      r[u] = rank[p0 + int64_t(d) * HW];
+      dp[u] = depth[p0 + int64_t(d) * HW];
+    }
+    float gv[kU][kCPL];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i) {
+        const int c = lane + 64 * i;
+        const int rr = r[u] >= 0 ? r[u] : 0;
+        const float v = g[int64_t(rr) * C + (c < C ? c : 0)];
+        gv[u][i] = (r[u] >= 0 && c < C) ? v : 0.0f;
+      }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (d0 + u < D) {
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCPL; ++i) part += gv[u][i] * xc[i];
+        const float dot = wave_sum(part);
+        if (lane == 0) grad_depth[p0 + int64_t(d0 + u) * HW] = r[u] >= 0 ? dot : 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCPL; ++i) gc[i] += gv[u][i] * dp[u];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kCPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < C) grad_ctx[bn * gsbn + int64_t(c) * gsc + hw] = gc[i];
   }
 }
 
@@ -1572,11 +1718,20 @@ bool bev_vec_ok(const void *base, size_t es, int64_t n_xy, int64_t sb, int64_t s
 template <typename T, int kCPL>
 int launch_accum_pipe_t(int slots, unsigned grid, size_t smem, hipStream_t s, const char *x,
                         int64_t ld_bytes, int C, int CB, const uint64_t *keys,
-                        const int32_t *meta, const int32_t *cend, float *acc) {
+                        const int32_t *meta, const int32_t *cend, float *acc,
+                        const DepthRows &dr) {
 #define BEVPOOL_PIPE_CASE(K)                                                                   \
   case K:                                                                                      \
-    hipLaunchKernelGGL((accum_pipe_kernel<T, K, kCPL>), dim3(grid), dim3(kPipeThreads), smem,  \
-                       s, x, ld_bytes, C, CB, keys, meta, cend, acc, kRangePoints);            \
+    if constexpr (std::is_same<T, F32>::value) { /* depth-weighted rows are fp32 only */       \
+      if (dr.depth) {                                                                          \
+        hipLaunchKernelGGL((accum_pipe_kernel<T, K, kCPL, true>), dim3(grid),                  \
+                           dim3(kPipeThreads), smem, s, x, ld_bytes, C, CB, keys, meta, cend,  \
+                           acc, kRangePoints, dr);                                            \
+        break;                                                                                 \
+      }                                                                                        \
+    }                                                                                          \
+    hipLaunchKernelGGL((accum_pipe_kernel<T, K, kCPL, false>), dim3(grid), dim3(kPipeThreads), \
+                       smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc, kRangePoints, dr);  \
     break;
   switch (slots) {
     BEVPOOL_PIPE_CASE(1)
@@ -1603,9 +1758,10 @@ int pipe_cpl(int CB) {
 
 int launch_accum_pipe(int32_t dtype, int slots, unsigned grid, size_t smem, hipStream_t s,
                       const char *x, int64_t ld_bytes, int C, int CB, const uint64_t *keys,
-                      const int32_t *meta, const int32_t *cend, float *acc) {
+                      const int32_t *meta, const int32_t *cend, float *acc,
+                      const DepthRows &dr) {
   const int cpl = pipe_cpl(CB);
-#define BEVPOOL_PIPE_ARGS slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc
+#define BEVPOOL_PIPE_ARGS slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc, dr
 #define BEVPOOL_PIPE_DTYPE(T)                                                                  \
   return cpl == 1   ? launch_accum_pipe_t<T, 1>(BEVPOOL_PIPE_ARGS)                            \
          : cpl == 2 ? launch_accum_pipe_t<T, 2>(BEVPOOL_PIPE_ARGS)                            \
@@ -1620,6 +1776,94 @@ int launch_accum_pipe(int32_t dtype, int slots, unsigned grid, size_t smem, hipS
   }
 #undef BEVPOOL_PIPE_DTYPE
 #undef BEVPOOL_PIPE_ARGS
+}
+
+// Pipelined forward accumulation (16-byte rows) into cell-major fp32 rows.
+int launch_forward_pipe(int32_t dtype, const char *x, int64_t ld_bytes, int C, int64_t n_points,
+                        const uint64_t *keys, const int32_t *meta, const int32_t *cend,
+                        float *acc, const DepthRows &dr, hipStream_t s) {
+  const size_t es = dtype_size(dtype);
+  // plain block order: ranges that run at the same time then read rows from
+  // one window of the feature tensor (an XCD-contiguous order measured slower)
+  const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
+  // channel block of at most 384 bytes per row: <= 6 16-byte slots per thread per
+  // stage and two stages + ranks/weights in <= 48.5 KB of LDS
+  const int CBmax = int(384 / es);
+  const int CB = C < CBmax ? C : CBmax;
+  const int rowq = int(size_t(CB) * es / 16);
+  const int slots = (kStageRows * rowq + kLoaders - 1) / kLoaders;
+  const size_t smem = size_t(2) * kStageRows * rowq * 16 + size_t(4) * kStageRows * sizeof(int);
+  if (smem > 65536) return fail(BEVPOOL_EINVAL, "internal: %zu bytes of LDS", smem);
+  LaunchTimer t("accum_rows", s);
+  return launch_accum_pipe(dtype, slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc,
+                           dr);
+}
+
+// cell-major fp32 rows -> channel-first output (zeros for empty cells).
+int launch_rows_to_bev(const float *acc, int32_t dtype, int C, const int32_t *cell_start,
+                       const int32_t *cell_end, int64_t n_cells, int n_z, int64_t n_xy,
+                       int64_t out_stride_b, int64_t out_stride_c, int64_t out_stride_z, void *out,
+                       hipStream_t s) {
+  const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
+  const int CT = C < kTileChannels ? C : kTileChannels;
+  const size_t es = dtype_size(dtype);
+  const size_t smem = size_t(kCellTile) * size_t(CT + 1) * sizeof(uint32_t);
+  const bool vrow = (C % 4 == 0) && (CT % 4 == 0) && (reinterpret_cast<uintptr_t>(acc) % 16 == 0);
+  const bool vbev = bev_vec_ok(out, es, n_xy, out_stride_b, out_stride_c, out_stride_z);
+  LaunchTimer t("rows_to_bev", s);
+#define BEVPOOL_R2B(T, VR, VB)                                                                 \
+  hipLaunchKernelGGL((rows_to_bev_kernel<T, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,    \
+                     acc, C, CT, cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b,       \
+                     out_stride_c, out_stride_z, static_cast<T::raw *>(out))
+#define BEVPOOL_R2B_T(T)                                                                       \
+  if (vrow && vbev) BEVPOOL_R2B(T, true, true);                                               \
+  else if (vrow) BEVPOOL_R2B(T, true, false);                                                 \
+  else if (vbev) BEVPOOL_R2B(T, false, true);                                                 \
+  else BEVPOOL_R2B(T, false, false);
+  switch (dtype) {
+    case BEVPOOL_F32:
+      BEVPOOL_R2B_T(F32)
+      break;
+    case BEVPOOL_F16:
+      BEVPOOL_R2B_T(F16)
+      break;
+    default:
+      BEVPOOL_R2B_T(BF16)
+      break;
+  }
+#undef BEVPOOL_R2B_T
+#undef BEVPOOL_R2B
+  return check_launch("rows_to_bev");
+}
+
+// channel-first gradient -> cell-major rows of the occupied cells (raw bits).
+int launch_bev_to_rows(const void *grad, size_t es, int64_t gsb, int64_t gsc, int64_t gsz, int C,
+                       const int32_t *cell_start, const int32_t *cell_end, int64_t n_cells,
+                       int n_z, int64_t n_xy, void *rows, hipStream_t s) {
+  const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
+  const int CT = C < kTileChannels ? C : kTileChannels;
+  const size_t smem = size_t(kCellTile) * size_t(CT + 1) * es;
+  const bool vrow = (size_t(C) * es % 16 == 0) && (size_t(CT) * es % 16 == 0) &&
+                    (reinterpret_cast<uintptr_t>(rows) % 16 == 0);
+  const bool vbev = bev_vec_ok(grad, es, n_xy, gsb, gsc, gsz);
+  LaunchTimer t("bev_to_rows", s);
+#define BEVPOOL_B2R(TR, VR, VB)                                                                \
+  hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,   \
+                     static_cast<const TR *>(grad), C, CT, cell_start, cell_end, n_cells, n_z, \
+                     n_xy, gsb, gsc, gsz, static_cast<TR *>(rows))
+#define BEVPOOL_B2R_T(TR)                                                                      \
+  if (vrow && vbev) BEVPOOL_B2R(TR, true, true);                                              \
+  else if (vrow) BEVPOOL_B2R(TR, true, false);                                                \
+  else if (vbev) BEVPOOL_B2R(TR, false, true);                                                \
+  else BEVPOOL_B2R(TR, false, false);
+  if (es == 4) {
+    BEVPOOL_B2R_T(uint32_t)
+  } else {
+    BEVPOOL_B2R_T(uint16_t)
+  }
+#undef BEVPOOL_B2R_T
+#undef BEVPOOL_B2R
+  return check_launch("bev_to_rows");
 }
 
 }  // namespace
@@ -1851,18 +2095,9 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
     // one window of the feature tensor (an XCD-contiguous order measured slower)
     const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
     if (vec16) {
-      // channel block of at most 384 bytes per row: <= 6 16-byte slots per thread per
-      // stage and two stages + ranks in <= 48.5 KB of LDS (three blocks per CU)
-      const int CBmax = int(384 / es);
-      const int CB = C < CBmax ? C : CBmax;
-      const int rowq = int(size_t(CB) * es / 16);
-      const int slots = (kStageRows * rowq + kLoaders - 1) / kLoaders;
-      const size_t smem = size_t(2) * kStageRows * rowq * 16 + size_t(2) * kStageRows * sizeof(int);
-      if (smem > 65536) return fail(BEVPOOL_EINVAL, "internal: %zu bytes of LDS", smem);
-      LaunchTimer t("accum_rows", s);
-      st = launch_accum_pipe(dtype, slots, grid, smem, s, static_cast<const char *>(feats),
-                             int64_t(size_t(feats_row_stride) * es), C, CB, keys, meta, cell_end,
-                             acc);
+      st = launch_forward_pipe(dtype, static_cast<const char *>(feats),
+                               int64_t(size_t(feats_row_stride) * es), C, n_points, keys, meta,
+                               cell_end, acc, DepthRows{nullptr, 0u, 0u}, s);
       if (st) return st;
     } else {
       const int CB = C < kThreads ? C : kThreads;
@@ -1891,36 +2126,101 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
       if ((st = check_launch("accum_rows"))) return st;
     }
   }
-  const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
+  return launch_rows_to_bev(acc, dtype, C, cell_start, cell_end, n_cells, n_z, n_xy,
+                            out_stride_b, out_stride_c, out_stride_z, out, s);
+}
+
+int bevpool_context_rows(const float *context, int64_t stride_bn, int64_t stride_c, int32_t BN,
+                         int32_t C, int64_t HW, float *rows, void *stream) {
+  g_last_error.clear();
+  if (BN < 0 || C < 1 || HW < 0) return fail(BEVPOOL_EINVAL, "bad context shape");
+  const int64_t n_pix = int64_t(BN) * HW;
+  if (n_pix == 0) return BEVPOOL_OK;
+  if (!context || !rows) return fail(BEVPOOL_EINVAL, "null argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
   const int CT = C < kTileChannels ? C : kTileChannels;
-  const size_t es = dtype_size(dtype);
-  const size_t smem = size_t(kCellTile) * size_t(CT + 1) * sizeof(uint32_t);
-  const bool vrow = (C % 4 == 0) && (CT % 4 == 0) && (reinterpret_cast<uintptr_t>(acc) % 16 == 0);
-  const bool vbev = bev_vec_ok(out, es, n_xy, out_stride_b, out_stride_c, out_stride_z);
-  LaunchTimer t("rows_to_bev", s);
-#define BEVPOOL_R2B(T, VR, VB)                                                                 \
-  hipLaunchKernelGGL((rows_to_bev_kernel<T, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,    \
-                     acc, C, CT, cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b,       \
-                     out_stride_c, out_stride_z, static_cast<T::raw *>(out))
-#define BEVPOOL_R2B_T(T)                                                                       \
-  if (vrow && vbev) BEVPOOL_R2B(T, true, true);                                               \
-  else if (vrow) BEVPOOL_R2B(T, true, false);                                                 \
-  else if (vbev) BEVPOOL_R2B(T, false, true);                                                 \
-  else BEVPOOL_R2B(T, false, false);
-  switch (dtype) {
-    case BEVPOOL_F32:
-      BEVPOOL_R2B_T(F32)
-      break;
-    case BEVPOOL_F16:
-      BEVPOOL_R2B_T(F16)
-      break;
-    default:
-      BEVPOOL_R2B_T(BF16)
-      break;
+  const size_t smem = size_t(kCellTile) * size_t(CT + 1) * sizeof(float);
+  LaunchTimer t("context_rows", s);
+  hipLaunchKernelGGL(context_rows_kernel, dim3(unsigned(ceil_div(n_pix, kCellTile))),
+                     dim3(kThreads), smem, s, context, C, HW, n_pix, stride_bn, stride_c, rows);
+  return check_launch("context_rows");
+}
+
+int bevpool_forward_depth(const float *depth, const float *context_rows, int32_t C,
+                          int64_t n_points, int32_t D, int64_t HW, const uint64_t *keys,
+                          const int32_t *cell_start, const int32_t *cell_end,
+                          const int32_t *meta, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                          int64_t out_stride_b, int64_t out_stride_c, int64_t out_stride_z,
+                          float *out, void *scratch, size_t scratch_bytes, void *stream) {
+  g_last_error.clear();
+  if (C < 1 || C % 4 != 0) return fail(BEVPOOL_EINVAL, "C must be a positive multiple of 4");
+  if (D < 1 || HW < 1) return fail(BEVPOOL_EINVAL, "bad depth layout (D=%d, HW=%lld)", D,
+                                   (long long)HW);
+  if (n_batch < 1 || n_z < 1 || n_xy < 1) return fail(BEVPOOL_EINVAL, "bad grid");
+  const int64_t n_cells = int64_t(n_batch) * n_z * n_xy;
+  if (n_cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "too many cells");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX) || n_points % (int64_t(D) * HW) != 0)
+    return fail(BEVPOOL_EINVAL, "n_points must be a multiple of D*HW");
+  if (!out || !cell_start || !cell_end || !meta) return fail(BEVPOOL_EINVAL, "null argument");
+  if (n_points > 0 && (!depth || !context_rows || !keys))
+    return fail(BEVPOOL_EINVAL, "null depth/context/keys");
+  if (reinterpret_cast<uintptr_t>(context_rows) % 16 != 0)
+    return fail(BEVPOOL_EINVAL, "context rows must be 16-byte aligned");
+  if (scratch_bytes < bevpool_forward_scratch_bytes(n_cells, C) || !scratch)
+    return fail(BEVPOOL_ESPACE, "forward scratch too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float *acc = static_cast<float *>(scratch);
+  int st;
+  if (n_points > 0) {
+    const DepthRows dr{depth, uint32_t(int64_t(D) * HW), uint32_t(HW)};
+    st = launch_forward_pipe(BEVPOOL_F32, reinterpret_cast<const char *>(context_rows),
+                             int64_t(C) * 4, C, n_points, keys, meta, cell_end, acc, dr, s);
+    if (st) return st;
   }
-#undef BEVPOOL_R2B_T
-#undef BEVPOOL_R2B
-  return check_launch("rows_to_bev");
+  return launch_rows_to_bev(acc, BEVPOOL_F32, C, cell_start, cell_end, n_cells, n_z, n_xy,
+                            out_stride_b, out_stride_c, out_stride_z, out, s);
+}
+
+int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t grad_stride_c,
+                           int64_t grad_stride_z, int32_t C, const int32_t *rank,
+                           int64_t n_points, int32_t D, int64_t HW, const float *depth,
+                           const float *context_rows, const int32_t *cell_start,
+                           const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                           float *grad_depth, float *grad_context, int64_t gctx_stride_bn,
+                           int64_t gctx_stride_c, void *scratch, size_t scratch_bytes,
+                           void *stream) {
+  g_last_error.clear();
+  if (C < 1 || C > 256) return fail(BEVPOOL_EINVAL, "C must be in [1, 256]");
+  if (D < 1 || HW < 1) return fail(BEVPOOL_EINVAL, "bad depth layout");
+  if (n_batch < 1 || n_z < 1 || n_xy < 1) return fail(BEVPOOL_EINVAL, "bad grid");
+  const int64_t n_cells = int64_t(n_batch) * n_z * n_xy;
+  if (n_cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "too many cells");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX) || n_points % (int64_t(D) * HW) != 0)
+    return fail(BEVPOOL_EINVAL, "n_points must be a multiple of D*HW");
+  if (n_points == 0) return BEVPOOL_OK;
+  if (!grad || !rank || !depth || !context_rows || !cell_start || !cell_end || !grad_depth ||
+      !grad_context)
+    return fail(BEVPOOL_EINVAL, "null argument");
+  if (!scratch || scratch_bytes < bevpool_backward_scratch_bytes(n_cells, C, BEVPOOL_F32))
+    return fail(BEVPOOL_ESPACE, "backward scratch too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int st;
+  if ((st = launch_bev_to_rows(grad, 4, grad_stride_b, grad_stride_c, grad_stride_z, C,
+                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
+    return st;
+  const int64_t n_pix = n_points / D;
+  const unsigned grid = unsigned(ceil_div(n_pix, kThreads / 64));
+  LaunchTimer t("depth_grad", s);
+  const float *g = static_cast<const float *>(scratch);
+#define BEVPOOL_DG(CPL)                                                                        \
+  hipLaunchKernelGGL((depth_grad_kernel<CPL, 8>), dim3(grid), dim3(kThreads), 0, s, g, C, rank, \
+                     depth, context_rows, D, HW, n_pix, grad_depth, grad_context,              \
+                     gctx_stride_bn, gctx_stride_c)
+  if (C <= 64) BEVPOOL_DG(1);
+  else if (C <= 128) BEVPOOL_DG(2);
+  else BEVPOOL_DG(4);
+#undef BEVPOOL_DG
+  return check_launch("depth_grad");
 }
 
 size_t bevpool_backward_scratch_bytes(int64_t n_cells, int32_t C, int32_t dtype) {
@@ -1951,8 +2251,7 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
     return fail(BEVPOOL_ESPACE, "backward scratch too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t es = dtype_size(dtype);
-  const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
-  // gather layout (decided first: the warm-up in bev_to_rows mirrors it)
+  // gather layout (decided first: the warm-up blocks mirror it)
   const size_t row_bytes = size_t(C) * es;
   const bool vec16 = (row_bytes % 16 == 0) && ((size_t(x_grad_row_stride) * es) % 16 == 0) &&
                      (reinterpret_cast<uintptr_t>(x_grad) % 16 == 0) &&
@@ -1962,34 +2261,10 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
   const unsigned grid = xcd_grid(ceil_div(total, int64_t(kThreads) * kGatherPer));
   const bool narrow = total < (int64_t(1) << 32);
   int st;
-  {
-    const int CT = C < kTileChannels ? C : kTileChannels;
-    const size_t smem = size_t(kCellTile) * size_t(CT + 1) * es;
-    const bool vrow = (size_t(C) * es % 16 == 0) && (size_t(CT) * es % 16 == 0) &&
-                      (reinterpret_cast<uintptr_t>(scratch) % 16 == 0);
-    const bool vbev =
-        bev_vec_ok(grad, es, n_xy, grad_stride_b, grad_stride_c, grad_stride_z);
-    LaunchTimer t("bev_to_rows", s);
-#define BEVPOOL_B2R(TR, VR, VB)                                                                \
-  hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,   \
-                     static_cast<const TR *>(grad), C, CT, cell_start, cell_end, n_cells, n_z, \
-                     n_xy, grad_stride_b, grad_stride_c, grad_stride_z,                        \
-                     static_cast<TR *>(scratch))
-#define BEVPOOL_B2R_T(TR)                                                                      \
-  if (vrow && vbev) BEVPOOL_B2R(TR, true, true);                                              \
-  else if (vrow) BEVPOOL_B2R(TR, true, false);                                                \
-  else if (vbev) BEVPOOL_B2R(TR, false, true);                                                \
-  else BEVPOOL_B2R(TR, false, false);
-    if (es == 4) {
-      BEVPOOL_B2R_T(uint32_t)
-    } else {
-      BEVPOOL_B2R_T(uint16_t)
-    }
-#undef BEVPOOL_B2R_T
-#undef BEVPOOL_B2R
-    if ((st = check_launch("bev_to_rows"))) return st;
-  }
-  // cache warm-up (see gather_warm_kernel): ranks per XCD + occupied rows
+  if ((st = launch_bev_to_rows(grad, es, grad_stride_b, grad_stride_c, grad_stride_z, C,
+                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
+    return st;
+  // cache warm-up (gather_warm_block): ranks per XCD + occupied rows
   GatherWarm w{};
   int rank_blocks = 0;
   if (BEVPOOL_XCD_MAP && reinterpret_cast<uintptr_t>(rank) % 16 == 0 && n_points >= 4) {
@@ -2008,16 +2283,6 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
     row_blocks = int(ceil_div(n_cells, kWarmCells));
   }
   int warm_blocks = rank_blocks + row_blocks;
-#if BEVPOOL_SEPARATE_WARM
-  if (warm_blocks > 0) {
-    LaunchTimer t("gather_warm", s);
-    hipLaunchKernelGGL(gather_warm_kernel, dim3(unsigned(warm_blocks)), dim3(kThreads), 0, s, w,
-                       n_points, cell_start, cell_end, n_cells, 0,
-                       static_cast<uint32_t *>(scratch));
-    if ((st = check_launch("gather_warm"))) return st;
-  }
-  warm_blocks = 0;
-#endif
   warm_blocks = int(ceil_div(warm_blocks, kXcds) * kXcds);  // keep XCD parity
   LaunchTimer t("gather_rows", s);
 #define BEVPOOL_GATHER(V, NARROW, LD)                                                          \

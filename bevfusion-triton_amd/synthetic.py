@@ -107,7 +107,7 @@ class Case:
     name: str
     spec: RigSpec
     geom: torch.Tensor  # (B, N, D, fH, fW, 3) fp32 (CPU)
-    x: torch.Tensor  # (B, N, D, fH, fW, C) channel-last contiguous
+    x: torch.Tensor | None  # (B, N, D, fH, fW, C) channel-last contiguous
     xbound: tuple = field(default=())
     ybound: tuple = field(default=())
     zbound: tuple = field(default=())
@@ -160,8 +160,10 @@ def make_features(spec: RigSpec, device='cpu', seed: int = 0) -> torch.Tensor:
     return x
 
 
-def make_case(name: str, device='cpu', seed: int = 0) -> Case:
+def make_case(name: str, device='cpu', seed: int = 0, features: bool = True) -> Case:
+    """Geometry and (unless ``features`` is False: then ``x`` is None) the
+    materialised feature of a named configuration."""
     spec = CASES[name]
     geom = make_geometry(spec)
-    x = make_features(spec, device=device, seed=seed)
+    x = make_features(spec, device=device, seed=seed) if features else None
     return Case(name, spec, geom, x, spec.xbound, spec.ybound, spec.zbound)

@@ -6,7 +6,9 @@ Drop-in for the pooling half of ``models/vtransforms/base.py``:
     ``BaseTransform.__init__`` (``base.py:57-60``) and its ``bev_pool(geom_feats, x)``
     method (``base.py:131-165``): quantise, batch index, kept mask,
     compaction, ``bev_pool``, Z-collapse;
-  * :func:`lss_bev_pool`         -- the same as a function.
+  * :func:`lss_bev_pool`         -- the same as a function;
+  * :func:`lss_bev_pool_depth`   -- the same for the LSS feature
+    ``depth (x) context`` (``depth_lss.py:91-94``) without materialising it.
 
 Everything between the geometry/feature tensors and the BEV map runs as HIP
 kernels: the quantisation/kept-mask, the compaction (fused into the first
@@ -98,6 +100,77 @@ def lss_bev_pool(geom_feats, x, dx, bx, nx, *, grid=None):
     return _LSSBevPool.apply(x, geom_feats, offset, d, tuple(n))
 
 
+class _LSSBevPoolDepth(torch.autograd.Function):
+    """Pooling of the outer product depth (x) context without materialising
+    it: point p = (bn*D + d)*HW + hw carries depth[bn, d, hw] * context[bn, :, hw]."""
+
+    @staticmethod
+    def forward(ctx, depth, context, geom_feats, B, offset, dx, nx):
+        BN, D, fH, fW = depth.shape
+        C = context.shape[1]
+        HW = fH * fW
+        X, Y, Z = nx
+        depth_flat = depth.contiguous().view(-1)
+        rows = P.context_rows(context.reshape(BN, C, HW))
+        idx = P.index_from_geom(geom_feats.reshape(-1, 3), B, offset, dx, nx)
+        out = torch.empty((B, Z * C, X, Y), dtype=torch.float32, device=depth.device)
+        P.forward_depth(idx, depth_flat, rows, D, HW, out, Z * C * X * Y, X * Y, C * X * Y)
+        ctx.pool_index = idx
+        ctx.save_for_backward(depth_flat, rows)
+        ctx.shapes = (BN, D, fH, fW, C)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        idx = ctx.pool_index
+        depth_flat, rows = ctx.saved_tensors
+        BN, D, fH, fW, C = ctx.shapes
+        if g.dtype != torch.float32:
+            g = g.float()
+        if g.stride(3) != 1 or g.stride(2) != idx.W:
+            g = g.contiguous()
+        grad_depth = torch.empty((BN, D, fH, fW), dtype=torch.float32, device=g.device)
+        grad_context = torch.empty((BN, C, fH, fW), dtype=torch.float32, device=g.device)
+        P.backward_depth(idx, g, C, g.stride(0), g.stride(1), C * g.stride(1), depth_flat, rows,
+                         D, fH * fW, grad_depth.view(-1), grad_context.view(BN, C, fH * fW))
+        return grad_depth, grad_context, None, None, None, None, None
+
+
+def lss_bev_pool_depth(geom_feats, depth, context, dx, bx, nx, *, grid=None):
+    """``lss_bev_pool(geom_feats, x, ...)`` for the LSS feature
+    ``x = depth.unsqueeze(1) * context.unsqueeze(2)`` rearranged to
+    (B, N, D, fH, fW, C) (``depth_lss.py:91-94``), without forming ``x``.
+
+    geom_feats (B, N, D, fH, fW, 3); depth (B*N, D, fH, fW) -- the softmaxed
+    depth distribution; context (B*N, C, fH, fW), any view whose (fH, fW)
+    plane is contiguous (the slice ``x[:, D:D+C]`` of the depth-net output
+    costs no copy).  Returns the same (B, C*Dz, H, W) fp32 map, bit for bit,
+    as pooling the materialised product; gradients flow to depth and
+    context.  Channel counts the fused kernels do not take (C not a multiple
+    of 4, or C > 256) pool the product formed on the GPU instead.
+    """
+    P.require_gpu(geom_feats, depth, context)
+    if depth.dim() != 4 or context.dim() != 4 or geom_feats.dim() != 6 \
+            or geom_feats.shape[-1] != 3:
+        raise ValueError('expected geom_feats (B, N, D, H, W, 3), depth (B*N, D, H, W) and '
+                         'context (B*N, C, H, W)')
+    B, N, D, fH, fW = geom_feats.shape[:5]
+    if tuple(depth.shape) != (B * N, D, fH, fW):
+        raise ValueError('depth must be (B*N, D, H, W) matching geom_feats')
+    if context.shape[0] != B * N or tuple(context.shape[2:]) != (fH, fW):
+        raise ValueError('context must be (B*N, C, H, W) matching geom_feats')
+    depth = depth.float()
+    context = context.float()
+    geom_feats = geom_feats.float()
+    C = context.shape[1]
+    offset, d, n = grid if grid is not None else host_grid(dx, bx, nx)
+    if C % 4 != 0 or C > 256 or C == 0:
+        x = depth.unsqueeze(1) * context.unsqueeze(2)  # (BN, C, D, fH, fW)
+        x = x.permute(0, 2, 3, 4, 1).reshape(B, N, D, fH, fW, C)
+        return _LSSBevPool.apply(x, geom_feats, offset, d, tuple(n))
+    return _LSSBevPoolDepth.apply(depth, context, geom_feats, B, offset, d, tuple(n))
+
+
 class BevPoolTransform(nn.Module):
     """The pooling state and method of ``BaseTransform`` (``base.py:26-66,
     131-165``): ``dx``, ``bx``, ``nx`` parameters from the x/y/z bounds and
@@ -127,6 +200,10 @@ class BevPoolTransform(nn.Module):
 
     def bev_pool(self, geom_feats, x):
         return lss_bev_pool(geom_feats, x, self.dx, self.bx, self.nx, grid=self.grid())
+
+    def bev_pool_depth(self, geom_feats, depth, context):
+        return lss_bev_pool_depth(geom_feats, depth, context, self.dx, self.bx, self.nx,
+                                  grid=self.grid())
 
     def forward(self, geom_feats, x):
         return self.bev_pool(geom_feats, x)

@@ -199,6 +199,75 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                      size_t scratch_bytes, void *stream);
 
 /*
+ * Depth-weighted (fused depth x context) pooling.  The reference builds the
+ * camera features as the outer product x[bn, c, d, h, w] =
+ * depth[bn, d, h, w] * context[bn, c, h, w] (models/vtransforms/depth_lss.py:
+ * 91-94, 638 MB at the det shape) and pools x; these calls pool
+ * depth[p] * context[pix(p), :] without materialising x.  Point p of the
+ * (B, N, D, fH, fW) frustum is p = (bn*D + d)*HW + hw with bn = b*N + n and
+ * HW = fH*fW; its context row is pix(p) = bn*HW + hw.  Ranks, keys and cell
+ * ranges come from bevpool_quantize_geom + bevpool_sort as for x.  Forward sums
+ * use the same products and order as the reference (fp32 product rounded,
+ * then added in point order), so they are bit-identical to pooling x.
+ */
+
+/*
+ * Context (BN, C, HW) fp32, element (bn, c, hw) at bn*stride_bn + c*stride_c
+ * + hw, to channel-last rows [BN*HW, C] (the layout the pooled rows are read
+ * in).  Replaces the context operand of depth_lss.py:92 (x[:, D:D+C], a
+ * channel-first slice of the depthnet output).
+ */
+int bevpool_context_rows(const float *context, int64_t stride_bn, int64_t stride_c, int32_t BN,
+                         int32_t C, int64_t HW, float *rows, void *stream);
+
+/*
+ * Forward of the depth-weighted pooling into the channel-first output, as
+ * bevpool_forward for x = depth (x) context.  Replaces depth_lss.py:91-94 followed
+ * by models/vtransforms/base.py:131-165 (bev_pool of the outer product).
+ *
+ *   depth         fp32 [n_points] = (BN, D, HW) contiguous
+ *   context_rows  fp32 [BN*HW, C] from bevpool_context_rows, 16-byte aligned;
+ *                 C a multiple of 4
+ *   n_points      BN * D * HW
+ *   scratch       >= bevpool_forward_scratch_bytes(n_cells, C) bytes
+ */
+int bevpool_forward_depth(const float *depth, const float *context_rows, int32_t C,
+                          int64_t n_points, int32_t D, int64_t HW, const uint64_t *keys,
+                          const int32_t *cell_start, const int32_t *cell_end,
+                          const int32_t *meta, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                          int64_t out_stride_b, int64_t out_stride_c, int64_t out_stride_z,
+                          float *out, void *scratch, size_t scratch_bytes, void *stream);
+
+/*
+ * Backward of the depth-weighted pooling: the reference's autograd through
+ * the outer product (depth_lss.py:93) and the pooling, without the [n_points,
+ * C] feature gradient:
+ *   grad_depth[p]           = sum_c g[cell(p), c] * context[pix(p), c]
+ *                             (0 for a dropped point)
+ *   grad_context[bn, c, hw] = sum_d g[cell(p_d), c] * depth[p_d]
+ *                             over the pixel's D points p_d (kept ones)
+ * Sums are fp32 in a fixed order (a butterfly over channels; d in order), so
+ * results are deterministic and agree with the reference within fp32
+ * rounding (the reference sums in torch's reduction order).
+ *
+ *   grad          fp32 BEV gradient; element (b, c, z, xy) at
+ *                 b*grad_stride_b + c*grad_stride_c + z*grad_stride_z + xy
+ *   C             <= 256
+ *   grad_depth    out: fp32 [n_points]
+ *   grad_context  out: fp32, element (bn, c, hw) at
+ *                 bn*gctx_stride_bn + c*gctx_stride_c + hw
+ *   scratch       >= bevpool_backward_scratch_bytes(n_cells, C, BEVPOOL_F32)
+ */
+int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t grad_stride_c,
+                           int64_t grad_stride_z, int32_t C, const int32_t *rank,
+                           int64_t n_points, int32_t D, int64_t HW, const float *depth,
+                           const float *context_rows, const int32_t *cell_start,
+                           const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                           float *grad_depth, float *grad_context, int64_t gctx_stride_bn,
+                           int64_t gctx_stride_c, void *scratch, size_t scratch_bytes,
+                           void *stream);
+
+/*
  * Optional per-kernel timing.  When enabled, every kernel launch is bracketed
  * by HIP events on the launch stream; bevpool_timing_read() synchronises
  * those events and returns, per kernel name, the summed milliseconds and

@@ -15,6 +15,11 @@ Pinning (see ``tests/test_oracle.py``):
   sort_perm        brute-force sorted((rank, index)) on tiny inputs.
   intervals        brute-force run-length encoding on tiny inputs.
   backward         brute-force gather on tiny inputs + the C restatement.
+  lss_feature      brute-force loops (one fp32 product per element) and the
+                   rearrange's index map on tiny inputs.
+  lss_bev_pool_depth  brute-force sequential fp32 loops of depth*context per
+                   cell; gradients against hand-written sums in float64 and
+                   against finite differences.
 """
 from __future__ import annotations
 
@@ -124,6 +129,30 @@ def lss_bev_pool(geom_feats, x, dx, bx, nx):
     xk = xf[q.kept]
     ck = q.coords[q.kept]
     out = bev_pool(xk, ck, B, int(nx[2]), int(nx[0]), int(nx[1]))
+    return torch.cat(out.unbind(dim=2), 1)
+
+
+def lss_feature(depth, context, B, N):
+    """``depth_lss.py:91-94``: x = depth.unsqueeze(1) * context.unsqueeze(2)
+    -> (BN, C, D, fH, fW), then ``rearrange('(b n) c d h w -> b n d h w c')``."""
+    x = depth.unsqueeze(1) * context.unsqueeze(2)
+    BN, C, D, fH, fW = x.shape
+    return x.permute(0, 2, 3, 4, 1).reshape(B, N, D, fH, fW, C)
+
+
+def lss_bev_pool_depth(geom_feats, depth, context, dx, bx, nx, dtype=torch.float32):
+    """The LSS feature (``lss_feature``) pooled by ``base.py:131-165``.
+    ``dtype`` float32 is the reference (``force_fp32``); float64 gives the
+    exact-arithmetic gradients the GPU's fp32 gradients are measured
+    against.  Differentiable in depth and context."""
+    B, N = geom_feats.shape[:2]
+    x = lss_feature(depth.to(dtype), context.to(dtype), B, N)
+    C = x.shape[-1]
+    q = quantize(geom_feats.float(), dx, bx, nx)
+    xk = x.reshape(-1, C)[q.kept]
+    ck = q.coords[q.kept]
+    out = bev_pool_cpu(xk, ck, B, int(nx[2]), int(nx[0]), int(nx[1]))
+    out = out.permute(0, 4, 1, 2, 3)
     return torch.cat(out.unbind(dim=2), 1)
 
 
