@@ -275,6 +275,8 @@ def main():
     # secondary op-level figure: bev_pool(feats (N_kept, C), coords (N_kept, 4))
     # on the kept points of the same geometry (ops/bev_pool/__init__.py entry)
     op = op_level(pkg, geom, x.detach(), module, dev)
+    # secondary figure: depth (x) context pooled fused vs materialised
+    fused = depth_fused(pkg, geom, module, spec, dev)
 
     # per-kernel durations from HIP events on the launch stream
     log(f'[bench] per-kernel timing over {args.profile_steps} steps')
@@ -367,6 +369,7 @@ def main():
             'avg_us': dom_us,
         },
         'op_level': op,
+        'depth_fused': fused,
         'kernels': kernels,
         'calibration': cal,
     }
@@ -415,6 +418,52 @@ def op_level(pkg, geom, x, module, dev):
             'n_points': int(feats.shape[0]), 'fwd_us': round(fwd * 1e3, 1),
             'bwd_us': round(bwd * 1e3, 1),
             'points_per_s': round(feats.shape[0] / ((fwd + bwd) * 1e-3), 1)}
+
+
+def depth_fused(pkg, geom, module, spec, dev):
+    """The LSS feature depth (x) context (depth_lss.py:91-94) from a depth-net
+    output (BN, D + C, fH, fW): pooled by lss_bev_pool_depth without forming
+    it, and materialised by the reference's product then pooled by
+    lss_bev_pool; fwd + autograd bwd to depth and context, median of 20."""
+    B, N, D, fH, fW = geom.shape[:5]
+    C = spec.channels
+    gen = torch.Generator(device=dev).manual_seed(1)
+    net = torch.randn(B * N, D + C, fH, fW, generator=gen, device=dev)
+    depth = net[:, :D].softmax(dim=1).requires_grad_(True)
+    context = net[:, D:D + C].detach().requires_grad_(True)
+    X, Y, Z = (int(v) for v in module.nx)
+    g = torch.randn((B, Z * C, X, Y), generator=gen, device=dev)
+
+    def fused():
+        return module.bev_pool_depth(geom, depth, context)
+
+    def materialised():
+        x = depth.unsqueeze(1) * context.unsqueeze(2)
+        return module.bev_pool(geom, x.permute(0, 2, 3, 4, 1).reshape(B, N, D, fH, fW, C))
+
+    res = {'what': 'depth (x) context -> BEV, fwd + autograd bwd to depth and context, '
+                   'median of 20 (materialised: torch product + lss_bev_pool)'}
+    for name, fn in (('fused', fused), ('materialised', materialised)):
+        for _ in range(3):
+            torch.autograd.grad(fn(), (depth, context), g)
+        evs = []
+        for _ in range(20):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record()
+            out = fn()
+            e[1].record()
+            torch.autograd.grad(out, (depth, context), g)
+            e[2].record()
+            evs.append(e)
+        torch.cuda.synchronize()
+        fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+        bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+        res[name] = {'fwd_us': round(fwd * 1e3, 1), 'bwd_us': round(bwd * 1e3, 1),
+                     'frustum_points_per_s': round(geom[..., 0].numel() / ((fwd + bwd) * 1e-3),
+                                                   1)}
+    res['speedup'] = round((res['materialised']['fwd_us'] + res['materialised']['bwd_us']) /
+                           (res['fused']['fwd_us'] + res['fused']['bwd_us']), 3)
+    return res
 
 
 def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):

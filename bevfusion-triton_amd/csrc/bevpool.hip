@@ -801,7 +801,27 @@ struct LoaderRing {
   int rk[kDepth];                // rank of row (lt % kStageRows) of a stage
   uint32_t dpi[kDepth];          // depth-weighted rows: point index of that row
   float dp[kDepth];              //   and its depth weight
+  int srow[kSlots];              // row of slot i within a stage (unclamped)
+  int sq[kSlots];                // 16-byte column of slot i
 };
+
+// n / d for n < 2^31 by multiply-high and shift (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", 1994): with
+// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (host side),
+// q = (mulhi(n, m) + n) >> s; mulhi(n, m) <= n keeps the sum in 32 bits.
+struct FastDiv {
+  uint32_t d, m, s;
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return (__umulhi(n, m) + n) >> s;
+  }
+};
+
+inline FastDiv make_fast_div(uint32_t d) {
+  uint32_t s = 0;
+  while ((uint64_t(1) << s) < d) ++s;
+  const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
+  return FastDiv{d, uint32_t(m), s};
+}
 
 // Rows of the depth-weighted forward (fused depth x context pooling): the row
 // of point p = (bn*D + d)*HW + hw is context row pix = bn*HW + hw, weighted by
@@ -809,10 +829,11 @@ struct LoaderRing {
 // models/vtransforms/depth_lss.py:91-94).
 struct DepthRows {
   const float *depth;  // (BN, D, HW) contiguous: depth[p]
-  uint32_t dhw, hw;    // D*HW, HW
+  FastDiv hw, nd;      // HW and D
+  // p = (bn*D + d)*HW + hw -> bn*HW + hw, with e = p / HW = bn*D + d
   __device__ __forceinline__ uint32_t pix(uint32_t p) const {
-    const uint32_t bn = p / dhw;
-    return bn * hw + (p - bn * dhw) % hw;
+    const uint32_t e = hw.div(p);
+    return nd.div(e) * hw.d + (p - e * hw.d);
   }
 };
 
@@ -826,8 +847,7 @@ __device__ __forceinline__ void ring_index(LoaderRing<kSlots> &R, int lt,
   const int64_t base = pr.s + int64_t(k) * kStageRows;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    int r = (lt + kLoaders * i) / pr.rowq;
-    r = r < rows - 1 ? r : rows - 1;
+    const int r = R.srow[i] < rows - 1 ? R.srow[i] : rows - 1;
     R.idx[j][i] = kw[2 * (rows > 0 ? base + r : pr.s)];  // low word: point index
   }
   if constexpr (kMul) {
@@ -848,8 +868,7 @@ __device__ __forceinline__ void ring_rows(LoaderRing<kSlots> &R, int lt,
   const bool live = pr.rows(k) > 0;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    const int slot = lt + kLoaders * i;
-    const int q = live ? slot - (slot / pr.rowq) * pr.rowq : 0;
+    const int q = live ? R.sq[i] : 0;
     const uint32_t row = kMul ? dr.pix(R.idx[j][i]) : R.idx[j][i];
     R.d[j][i] =
         *reinterpret_cast<const u32x4 *>(xb + int64_t(row) * ld_bytes + col_bytes + q * 16);
@@ -866,17 +885,40 @@ template <int kSlots, int j, bool kMul>
 __device__ __forceinline__ void ring_store(const LoaderRing<kSlots> &R, int lt,
                                            const PipeRange &pr, int k, u32x4 *__restrict__ lbuf,
                                            int *__restrict__ lrk) {
-  const int n = pr.rows(k) * pr.rowq;
+  const int rows = pr.rows(k);
+  const int n = rows * pr.rowq;
+  if constexpr (kMul) {
+    // slot i of this thread holds a piece of row srow[i]; lane r of every
+    // loader wave holds the depth weight of row r (ring_index / ring_rows):
+    // all lanes shuffle it in before any store is masked off, then scale the
+    // piece (one fp32 product per element, as the reference's product)
+    u32x4 v[kSlots];
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) {
-    const int slot = lt + kLoaders * i;
-    if (slot < n) lbuf[slot] = R.d[j][i];
+    for (int i = 0; i < kSlots; ++i) {
+      const int r = R.srow[i] < kStageRows - 1 ? R.srow[i] : kStageRows - 1;
+      const float w = __shfl(R.dp[j], r, 64);
+      // __uint_as_float takes the element by value: hipcc 7.2's
+      // __builtin_bit_cast of a vector element (v.y) reads element 0
+      const float x0 = __uint_as_float(R.d[j][i].x) * w;
+      const float x1 = __uint_as_float(R.d[j][i].y) * w;
+      const float x2 = __uint_as_float(R.d[j][i].z) * w;
+      const float x3 = __uint_as_float(R.d[j][i].w) * w;
+      v[i] = u32x4{__float_as_uint(x0), __float_as_uint(x1), __float_as_uint(x2),
+                   __float_as_uint(x3)};
+    }
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int slot = lt + kLoaders * i;
+      if (slot < n) lbuf[slot] = v[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int slot = lt + kLoaders * i;
+      if (slot < n) lbuf[slot] = R.d[j][i];
+    }
   }
-  if (lt < kStageRows) {
-    lrk[lt] = R.rk[j];
-    // depth weights follow the ranks (lrk + kStageRows)
-    if constexpr (kMul) lrk[kStageRows + lt] = __builtin_bit_cast(int, R.dp[j]);
-  }
+  if (lt < kStageRows) lrk[lt] = R.rk[j];
 }
 
 // One loader step k with ring slot r = k % kDepth (a template constant).
@@ -941,9 +983,6 @@ struct RowSum {
 
   // lb: the stage's rows in LDS (row stride cb elements), col: this lane's
   // columns; nch: channels of this wave (stores of lanes past nch are skipped).
-  // kMul: each row is first multiplied by its weight (fp32 bits at
-  // lrk[kStageRows + row]); product and sum are separate roundings.
-  template <bool kMul>
   __device__ __forceinline__ void add_stage(const typename T::raw *__restrict__ lb,
                                             const int *__restrict__ lrk, int rows, int cb,
                                             const int (&col)[kCPL], int nch,
@@ -961,14 +1000,6 @@ struct RowSum {
       for (int u = 0; u < kB; ++u)
 #pragma unroll
         for (int i = 0; i < kCPL; ++i) v[u][i] = T::load(lb + (j0 + u) * cb + col[i]);
-      if constexpr (kMul) {
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          const float wgt = __builtin_bit_cast(float, lrk[kStageRows + j0 + u]);
-#pragma unroll
-          for (int i = 0; i < kCPL; ++i) v[u][i] = v[u][i] * wgt;
-        }
-      }
       const uint32_t chunk = uint32_t(starts >> j0) & uint32_t((uint64_t(1) << kB) - 1);
       const bool full = j0 + kB <= rows;
       if (full && chunk == 0) {
@@ -1022,9 +1053,8 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
   const int rowq_max = CB * int(sizeof(raw)) / 16;
   u32x4 *buf0 = smem4;
   u32x4 *buf1 = smem4 + kStageRows * rowq_max;
-  // per stage buffer: kStageRows ranks, then kStageRows depth weights
   int *rk0s = reinterpret_cast<int *>(smem4 + 2 * kStageRows * rowq_max);
-  int *rk1s = rk0s + 2 * kStageRows;
+  int *rk1s = rk0s + kStageRows;
   const uint32_t *kw = reinterpret_cast<const uint32_t *>(keys);
 
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
@@ -1061,8 +1091,8 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
 #pragma unroll
         for (int r = 0; r < kDepth; ++r) {
           const int kk = k + r;
-          st.template add_stage<kMul>(reinterpret_cast<const raw *>((kk & 1) ? buf1 : buf0),
-                                      (kk & 1) ? rk1s : rk0s, pr.rows(kk), cb, col, nch, out, C);
+          st.add_stage(reinterpret_cast<const raw *>((kk & 1) ? buf1 : buf0),
+                       (kk & 1) ? rk1s : rk0s, pr.rows(kk), cb, col, nch, out, C);
           __syncthreads();
         }
       }
@@ -1070,6 +1100,12 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
     } else {
       const int col_bytes = c0 * int(sizeof(raw));
       LoaderRing<kSlots> R;
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        const int slot = lt + kLoaders * i;
+        R.srow[i] = slot / pr.rowq;
+        R.sq[i] = slot - R.srow[i] * pr.rowq;
+      }
       // prologue: indices of stages 0..D-1, rows of 0..D-1 each followed by the
       // indices of stage j+D; then stage 0 into LDS
 #define BEVPOOL_RING_PRO(J)                                                                    \
@@ -1564,74 +1600,157 @@ __global__ __launch_bounds__(kThreads) void context_rows_kernel(
   }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15) in a fixed order:
+// xor 1, xor 2 (quad permutes), then the half-row and row mirrors.  Each
+// step adds two equal-order partial sums, so every lane of the row ends with
+// the same value.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0x140, 0xF, 0xF, false));
   return v;
 }
+
+constexpr int kDgPix = 16;  // pixels per depth_grad block (4 per wave)
 
 // Backward of out[cell] = sum_{p in cell} depth[p] * ctx[pix(p)] (the
 // reference's autograd through depth_lss.py:91-94 and the pooling):
 //   grad_depth[p]        = sum_c g[rank[p], c] * ctx[pix(p), c]  (0 if dropped)
 //   grad_ctx[bn, c, hw]  = sum_d g[rank[p_d], c] * depth[p_d]
-// with p_d = (bn*D + d)*HW + hw.  One wave per pixel; lane l holds channels
-// l + 64 i (i < kCPL); the dot product is a fixed-order butterfly over the
-// wave, the context sum runs over d in order.  g: cell-major fp32 rows of the
-// occupied cells; ctx: channel-last rows (context_rows_kernel).
-template <int kCPL, int kU>
+// with p_d = (bn*D + d)*HW + hw.
+// A block takes kDgPix consecutive pixels.  Their ranks and depths are staged
+// in LDS ([d][pixel], read coalesced over the pixels); each wave then takes
+// kDgPix/4 pixels one after another, its four 16-lane rows taking the depth
+// bins d = 4 i + row, lane j of a row the channels j + 16 k (k < kK).  Per bin
+// a row gathers its cell's gradient row, reduces the dot product with
+// row_sum16 and adds depth * row to its context sums; the four rows' context
+// sums are combined in row order at the end of the pixel.  The dot products
+// replace the ranks in LDS and, like the context sums, are written out
+// coalesced.  g: cell-major fp32 rows of the occupied cells; ctx:
+// channel-last rows (context_rows_kernel).  Blocks map XCD-contiguously, so
+// the cells of neighbouring pixels' rays meet in one L2.
+template <int kK, int kU>
 __global__ __launch_bounds__(kThreads) void depth_grad_kernel(
     const float *__restrict__ g, int C, const int32_t *__restrict__ rank,
     const float *__restrict__ depth, const float *__restrict__ ctx, int D, int64_t HW,
-    int64_t n_pix, float *__restrict__ grad_depth, float *__restrict__ grad_ctx,
+    int64_t n_pix, uint32_t *__restrict__ grad_depth, float *__restrict__ grad_ctx,
     int64_t gsbn, int64_t gsc) {
-  const int lane = lane_id();
-  const int64_t pix = (int64_t(blockIdx.x) * kThreads + threadIdx.x) >> 6;
-  if (pix >= n_pix) return;  // whole wave
-  const int64_t bn = pix / HW, hw = pix - bn * HW;
-  float xc[kCPL], gc[kCPL];
-#pragma unroll
-  for (int i = 0; i < kCPL; ++i) {
-    const int c = lane + 64 * i;
-    xc[i] = c < C ? ctx[pix * C + c] : 0.0f;
-    gc[i] = 0.0f;
-  }
-  const int64_t p0 = bn * int64_t(D) * HW + hw;  // point of depth bin d: p0 + d * HW
-  for (int d0 = 0; d0 < D; d0 += kU) {
-    int r[kU];
-    float dp[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int d = d0 + u < D ? d0 + u : D - 1;
-      r[u] = rank[p0 + int64_t(d) * HW];
-      dp[u] = depth[p0 + int64_t(d) * HW];
+  extern __shared__ int dg_smem[];
+  int *lr = dg_smem;                                             // [D][kDgPix]
+  float *ldp = reinterpret_cast<float *>(dg_smem + D * kDgPix);  // [D][kDgPix]
+  float *lgc = ldp + D * kDgPix;                                 // [C][kDgPix]
+  const int tid = threadIdx.x;
+  const int64_t pix0 = xcd_chunk(blockIdx.x, gridDim.x) * kDgPix;
+  if (pix0 >= n_pix) return;  // XCD padding blocks
+  const int npx = n_pix - pix0 < kDgPix ? int(n_pix - pix0) : kDgPix;
+  for (int i = tid; i < D * kDgPix; i += kThreads) {
+    const int d = i / kDgPix, t = i - d * kDgPix;
+    int r = -1;
+    float dv = 0.0f;
+    if (t < npx) {
+      const int64_t pix = pix0 + t;
+      const int64_t bn = pix / HW, hw = pix - bn * HW;
+      const int64_t p = (bn * D + d) * HW + hw;
+      r = rank[p];
+      dv = depth[p];
     }
-    float gv[kU][kCPL];
+    lr[i] = r;
+    ldp[i] = dv;
+  }
+  __syncthreads();
+  const int lane = lane_id();
+  const int row = lane >> 4, j = lane & 15;
+  const int wave = tid >> 6;
+  int col[kK];
+  bool cv[kK];
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
+  for (int k = 0; k < kK; ++k) {
+    const int c = j + 16 * k;
+    cv[k] = c < C;
+    col[k] = cv[k] ? c : C - 1;
+  }
+  const int nrow = (D + 3) >> 2;  // bins per row
+  constexpr int kPerWave = kDgPix / kWaves;
+  for (int q = 0; q < kPerWave; ++q) {
+    const int t = wave * kPerWave + q;
+    if (t >= npx) break;  // wave-uniform
+    const int64_t pix = pix0 + t;
+    float xc[kK], gc[kK];
 #pragma unroll
-      for (int i = 0; i < kCPL; ++i) {
-        const int c = lane + 64 * i;
-        const int rr = r[u] >= 0 ? r[u] : 0;
-        const float v = g[int64_t(rr) * C + (c < C ? c : 0)];
-        gv[u][i] = (r[u] >= 0 && c < C) ? v : 0.0f;
+    for (int k = 0; k < kK; ++k) {
+      const float v = ctx[pix * C + col[k]];
+      xc[k] = cv[k] ? v : 0.0f;
+      gc[k] = 0.0f;
+    }
+    for (int i0 = 0; i0 < nrow; i0 += kU) {
+      int rr[kU];
+      float dp[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int d = 4 * (i0 + u) + row;
+        const int dc = d < D ? d : D - 1;
+        const int r = lr[dc * kDgPix + t];
+        const float w = ldp[dc * kDgPix + t];
+        rr[u] = d < D ? r : -1;
+        dp[u] = d < D ? w : 0.0f;
+      }
+      // every load is issued (clamped rows/columns) and masked by a bitwise
+      // AND afterwards: a select would let the compiler sink each load into
+      // a branch of its own and wait for it there
+      const uint32_t *gb = reinterpret_cast<const uint32_t *>(g);
+      float gv[kU][kK];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t base = int64_t(rr[u] >= 0 ? rr[u] : 0) * C;
+#pragma unroll
+        for (int k = 0; k < kK; ++k) {
+          const uint32_t m = (rr[u] >= 0 && cv[k]) ? 0xFFFFFFFFu : 0u;
+          gv[u][k] = __builtin_bit_cast(float, gb[base + col[k]] & m);
+        }
       }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (d0 + u < D) {
+      for (int u = 0; u < kU; ++u) {
         float part = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kCPL; ++i) part += gv[u][i] * xc[i];
-        const float dot = wave_sum(part);
-        if (lane == 0) grad_depth[p0 + int64_t(d0 + u) * HW] = r[u] >= 0 ? dot : 0.0f;
+        for (int k = 0; k < kK; ++k) part += gv[u][k] * xc[k];
+        const float dot = row_sum16(part);
+        const int d = 4 * (i0 + u) + row;
+        if (j == 0 && d < D) lr[d * kDgPix + t] = __builtin_bit_cast(int, rr[u] >= 0 ? dot : 0.0f);
 #pragma unroll
-        for (int i = 0; i < kCPL; ++i) gc[i] += gv[u][i] * dp[u];
+        for (int k = 0; k < kK; ++k) gc[k] += gv[u][k] * dp[u];
       }
     }
-  }
 #pragma unroll
-  for (int i = 0; i < kCPL; ++i) {
-    const int c = lane + 64 * i;
-    if (c < C) grad_ctx[bn * gsbn + int64_t(c) * gsc + hw] = gc[i];
+    for (int k = 0; k < kK; ++k) {
+      const float s0 = __shfl(gc[k], j, 64);
+      const float s1 = __shfl(gc[k], j + 16, 64);
+      const float s2 = __shfl(gc[k], j + 32, 64);
+      const float s3 = __shfl(gc[k], j + 48, 64);
+      const float tot = ((s0 + s1) + s2) + s3;
+      if (row == 0 && cv[k]) lgc[(j + 16 * k) * kDgPix + t] = tot;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < D * kDgPix; i += kThreads) {
+    const int d = i / kDgPix, t = i - d * kDgPix;
+    if (t < npx) {
+      const int64_t pix = pix0 + t;
+      const int64_t bn = pix / HW, hw = pix - bn * HW;
+      grad_depth[(bn * D + d) * HW + hw] = uint32_t(lr[i]);
+    }
+  }
+  for (int i = tid; i < C * kDgPix; i += kThreads) {
+    const int c = i / kDgPix, t = i - c * kDgPix;
+    if (t < npx) {
+      const int64_t pix = pix0 + t;
+      const int64_t bn = pix / HW, hw = pix - bn * HW;
+      grad_ctx[bn * gsbn + int64_t(c) * gsc + hw] = lgc[i];
+    }
   }
 }
 
@@ -1787,12 +1906,12 @@ int launch_forward_pipe(int32_t dtype, const char *x, int64_t ld_bytes, int C, i
   // one window of the feature tensor (an XCD-contiguous order measured slower)
   const unsigned grid = unsigned(ceil_div(n_points, kRangePoints));
   // channel block of at most 384 bytes per row: <= 6 16-byte slots per thread per
-  // stage and two stages + ranks/weights in <= 48.5 KB of LDS
+  // stage and two stages + ranks in <= 24.3 KB of LDS
   const int CBmax = int(384 / es);
   const int CB = C < CBmax ? C : CBmax;
   const int rowq = int(size_t(CB) * es / 16);
   const int slots = (kStageRows * rowq + kLoaders - 1) / kLoaders;
-  const size_t smem = size_t(2) * kStageRows * rowq * 16 + size_t(4) * kStageRows * sizeof(int);
+  const size_t smem = size_t(2) * kStageRows * rowq * 16 + size_t(2) * kStageRows * sizeof(int);
   if (smem > 65536) return fail(BEVPOOL_EINVAL, "internal: %zu bytes of LDS", smem);
   LaunchTimer t("accum_rows", s);
   return launch_accum_pipe(dtype, slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc,
@@ -2097,7 +2216,7 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
     if (vec16) {
       st = launch_forward_pipe(dtype, static_cast<const char *>(feats),
                                int64_t(size_t(feats_row_stride) * es), C, n_points, keys, meta,
-                               cell_end, acc, DepthRows{nullptr, 0u, 0u}, s);
+                               cell_end, acc, DepthRows{nullptr, {}, {}}, s);
       if (st) return st;
     } else {
       const int CB = C < kThreads ? C : kThreads;
@@ -2172,7 +2291,7 @@ int bevpool_forward_depth(const float *depth, const float *context_rows, int32_t
   float *acc = static_cast<float *>(scratch);
   int st;
   if (n_points > 0) {
-    const DepthRows dr{depth, uint32_t(int64_t(D) * HW), uint32_t(HW)};
+    const DepthRows dr{depth, make_fast_div(uint32_t(HW)), make_fast_div(uint32_t(D))};
     st = launch_forward_pipe(BEVPOOL_F32, reinterpret_cast<const char *>(context_rows),
                              int64_t(C) * 4, C, n_points, keys, meta, cell_end, acc, dr, s);
     if (st) return st;
@@ -2209,16 +2328,28 @@ int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t gra
                                cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
     return st;
   const int64_t n_pix = n_points / D;
-  const unsigned grid = unsigned(ceil_div(n_pix, kThreads / 64));
+  const size_t smem = size_t(2 * int64_t(D) + C) * kDgPix * sizeof(float);
+  if (smem > 65536)
+    return fail(BEVPOOL_EINVAL, "depth bins and channels too many (2*D + C = %lld > 1024)",
+                (long long)(2 * int64_t(D) + C));
+  const unsigned grid = xcd_grid(ceil_div(n_pix, kDgPix));
   LaunchTimer t("depth_grad", s);
   const float *g = static_cast<const float *>(scratch);
-#define BEVPOOL_DG(CPL)                                                                        \
-  hipLaunchKernelGGL((depth_grad_kernel<CPL, 8>), dim3(grid), dim3(kThreads), 0, s, g, C, rank, \
-                     depth, context_rows, D, HW, n_pix, grad_depth, grad_context,              \
-                     gctx_stride_bn, gctx_stride_c)
-  if (C <= 64) BEVPOOL_DG(1);
-  else if (C <= 128) BEVPOOL_DG(2);
-  else BEVPOOL_DG(4);
+  uint32_t *gd = reinterpret_cast<uint32_t *>(grad_depth);
+#define BEVPOOL_DG(K, U)                                                                       \
+  hipLaunchKernelGGL((depth_grad_kernel<K, U>), dim3(grid), dim3(kThreads), smem, s, g, C,     \
+                     rank, depth, context_rows, D, HW, n_pix, gd, grad_context, gctx_stride_bn, \
+                     gctx_stride_c)
+  const int kk = (C + 15) / 16;
+  if (kk <= 1) BEVPOOL_DG(1, 8);
+  else if (kk <= 2) BEVPOOL_DG(2, 8);
+  else if (kk <= 3) BEVPOOL_DG(3, 8);
+  else if (kk <= 4) BEVPOOL_DG(4, 8);
+  else if (kk <= 5) BEVPOOL_DG(5, 8);
+  else if (kk <= 6) BEVPOOL_DG(6, 8);
+  else if (kk <= 8) BEVPOOL_DG(8, 4);
+  else if (kk <= 12) BEVPOOL_DG(12, 4);
+  else BEVPOOL_DG(16, 4);
 #undef BEVPOOL_DG
   return check_launch("depth_grad");
 }
