@@ -277,6 +277,8 @@ def main():
     op = op_level(pkg, geom, x.detach(), module, dev)
     # secondary figure: depth (x) context pooled fused vs materialised
     fused = depth_fused(pkg, geom, module, spec, dev)
+    # secondary figure: channel-first (planar) features, the reference's layout
+    planar = channel_first(pkg, geom, module, x.detach(), g, dev)
 
     # per-kernel durations from HIP events on the launch stream
     log(f'[bench] per-kernel timing over {args.profile_steps} steps')
@@ -370,6 +372,7 @@ def main():
         },
         'op_level': op,
         'depth_fused': fused,
+        'channel_first': planar,
         'kernels': kernels,
         'calibration': cal,
     }
@@ -463,6 +466,44 @@ def depth_fused(pkg, geom, module, spec, dev):
                                                    1)}
     res['speedup'] = round((res['materialised']['fwd_us'] + res['materialised']['bwd_us']) /
                            (res['fused']['fwd_us'] + res['fused']['bwd_us']), 3)
+    return res
+
+
+def channel_first(pkg, geom, module, x, g, dev):
+    """Features in the reference's layout: the (B, N, D, fH, fW, C) view of
+    channel-first storage (depth_lss.py:94).  'planar': lss_bev_pool on the
+    view (one transposing kernel forward, gradient written channel-first);
+    'copy': torch's contiguous() copy (base.py:136 reshape) then the
+    channel-last path.  fwd + autograd bwd to the storage, median of 20."""
+    storage = x.permute(0, 1, 5, 2, 3, 4).contiguous().requires_grad_(True)
+
+    def planar():
+        return module.bev_pool(geom, storage.permute(0, 1, 3, 4, 5, 2))
+
+    def copy():
+        return module.bev_pool(geom, storage.permute(0, 1, 3, 4, 5, 2).contiguous())
+
+    res = {'what': 'x as the view of channel-first storage, fwd + autograd bwd to the storage, '
+                   'median of 20'}
+    for name, fn in (('planar', planar), ('copy', copy)):
+        for _ in range(3):
+            torch.autograd.grad(fn(), storage, g)
+        evs = []
+        for _ in range(20):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record()
+            out = fn()
+            e[1].record()
+            torch.autograd.grad(out, storage, g)
+            e[2].record()
+            evs.append(e)
+        torch.cuda.synchronize()
+        fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+        bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+        res[name] = {'fwd_us': round(fwd * 1e3, 1), 'bwd_us': round(bwd * 1e3, 1),
+                     'frustum_points_per_s': round(geom[..., 0].numel() / ((fwd + bwd) * 1e-3),
+                                                   1)}
+    del storage
     return res
 
 

@@ -68,6 +68,12 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     'bevpool_context_rows': ([_vp, _i64, _i64, _i32, _i32, _i64, _vp, _vp], ctypes.c_int),
+    'bevpool_planar_rows': ([_vp, _i64, _i64, _i32, _i32, _i64, _vp, _vp], ctypes.c_int),
+    'bevpool_backward_planar': (
+        [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i64, _i64, _vp, _i64,
+         _i64, _vp, _sz, _vp],
+        ctypes.c_int,
+    ),
     'bevpool_forward_depth': (
         [_vp, _vp, _i32, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64,
          _i64, _vp, _vp, _sz, _vp],

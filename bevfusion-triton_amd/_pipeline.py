@@ -244,21 +244,45 @@ def _backward_call(lib, idx, grad, dtype, C, stride_b, stride_c, stride_z, x_gra
 
 # ---- depth-weighted (fused depth x context) pooling -------------------------
 
-def context_rows(context3d):
-    """(BN, C, HW) fp32 context with HW contiguous -> (BN*HW, C) rows."""
-    BN, C, HW = context3d.shape
-    if context3d.stride(2) != 1:
-        context3d = context3d.contiguous()
-    rows = torch.empty((BN * HW, C), dtype=torch.float32, device=context3d.device)
-    with torch.cuda.device(context3d.device):
+def planar_rows(src3d):
+    """(BN, C, S) fp32 planar tensor (S contiguous, any batch/channel strides)
+    -> (BN*S, C) channel-last rows."""
+    BN, C, S = src3d.shape
+    if src3d.stride(2) != 1:
+        src3d = src3d.contiguous()
+    rows = torch.empty((BN * S, C), dtype=torch.float32, device=src3d.device)
+    with torch.cuda.device(src3d.device):
         L.check(
-            L.library().bevpool_context_rows(
-                L.ptr(context3d), context3d.stride(0), context3d.stride(1), BN, C, HW,
-                L.ptr(rows), L.stream_handle(context3d.device),
+            L.library().bevpool_planar_rows(
+                L.ptr(src3d), src3d.stride(0), src3d.stride(1), BN, C, S, L.ptr(rows),
+                L.stream_handle(src3d.device),
             ),
-            'bevpool_context_rows',
+            'bevpool_planar_rows',
         )
     return rows
+
+
+context_rows = planar_rows  # the depth-net context is planar with S = fH*fW
+
+
+def backward_planar(idx: PoolIndex, grad, C: int, stride_b: int, stride_c: int, stride_z: int,
+                    x_grad3d) -> None:
+    """Gradient of the pooling written straight into a planar (BN, C, S) fp32
+    tensor (S contiguous)."""
+    BN, _, S = x_grad3d.shape
+    lib = L.library()
+    scratch_bytes = lib.bevpool_backward_scratch_bytes(idx.n_cells, C, L.F32)
+    scratch = torch.empty(max(int(scratch_bytes), 256), dtype=torch.uint8, device=idx.device)
+    with torch.cuda.device(idx.device):
+        L.check(
+            lib.bevpool_backward_planar(
+                L.ptr(grad), stride_b, stride_c, stride_z, C, L.ptr(idx.rank), idx.n_points,
+                L.ptr(idx.cell_start), L.ptr(idx.cell_end), idx.B, idx.D, idx.H * idx.W, S,
+                L.ptr(x_grad3d), x_grad3d.stride(0), x_grad3d.stride(1), L.ptr(scratch),
+                scratch.numel(), L.stream_handle(idx.device),
+            ),
+            'bevpool_backward_planar',
+        )
 
 
 def forward_depth(idx: PoolIndex, depth_flat, rows, D: int, HW: int, out, stride_b: int,

@@ -28,8 +28,11 @@
 //                               cached; then a point-order streaming copy of
 //                               each point's cell row (zero rows for dropped
 //                               points)
+//   planar (channel-first) operands
+//     planar_rows_kernel        (BN, C, S) -> channel-last rows (context, or
+//                               channel-first camera features)
+//     gather_planar_kernel      backward straight into a (BN, C, S) gradient
 //   depth-weighted pooling (fused depth x context)
-//     context_rows_kernel       context (BN, C, HW) -> channel-last rows
 //     accum_pipe_kernel<..,true> forward sums of depth[p] * ctx[pix(p)]
 //     depth_grad_kernel         grad_depth (dot products) and grad_context
 //                               (depth-weighted sums along each ray)
@@ -1568,35 +1571,140 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
 // depth-weighted (fused depth x context) pooling helpers
 // ---------------------------------------------------------------------------
 
-// context (BN, C, HW), element (bn, c, hw) at bn*sbn + c*sc + hw (hw
-// contiguous), -> rows (BN*HW, C) fp32 channel-last; 64 pixels x up to
-// kTileChannels channels per pass through LDS.
-__global__ __launch_bounds__(kThreads) void context_rows_kernel(
-    const float *__restrict__ ctx, int C, int64_t HW, int64_t n_pix, int64_t sbn, int64_t sc,
-    float *__restrict__ rows) {
-  extern __shared__ float ctile[];  // kCellTile * (CT + 1)
-  const int tid = threadIdx.x;
-  const int64_t pix0 = int64_t(blockIdx.x) * kCellTile;
-  const int CT = C < kTileChannels ? C : kTileChannels;
-  const int pitch = CT + 1;
-  for (int c0 = 0; c0 < C; c0 += CT) {
-    const int cb = C - c0 < CT ? C - c0 : CT;
-    for (int i = tid; i < kCellTile * cb; i += kThreads) {
-      const int c = i / kCellTile, t = i - c * kCellTile;
-      const int64_t pix = pix0 + t;
-      float v = 0.0f;
-      if (pix < n_pix) {
-        const int64_t bn = pix / HW, hw = pix - bn * HW;
-        v = ctx[bn * sbn + int64_t(c0 + c) * sc + hw];
+// ---- planar (channel-first) <-> rows ---------------------------------------
+//
+// A planar tensor (BN, C, S) has element (bn, c, s) at bn*sbn + c*sc + s (s
+// contiguous): the depth-net context (S = fH*fW) and channel-first camera
+// features (S = D*fH*fW, the storage behind the reference's rearrange view,
+// depth_lss.py:94).  Point p = bn*S + s.
+
+// planar -> rows (BN*S, C), fp32.  Vector form (C, S, sbn, sc multiples of 4,
+// 16-byte aligned bases): a block covers 256 consecutive s of one bn; thread
+// (wave w, lane l) owns points s0 + [0, 4) and walks the channels in 4x4
+// blocks c0 + [0, 4) (c0 = 4 (l >> 4) + 16 i): four 16-byte loads along s (16
+// lanes of a channel read 256 contiguous bytes), a register transpose, four
+// 16-byte row stores (4 lanes write 64 contiguous bytes of a row; the wave
+// completes its 64 rows within one pass over the channels).  Non-temporal
+// stores: the rows are read back by a random gather, not from cache.  No LDS,
+// no barrier.  Scalar form: one element per thread.
+#ifndef BEVPOOL_PLANAR_NT
+#define BEVPOOL_PLANAR_NT 1
+#endif
+
+__device__ __forceinline__ void store16(u32x4 *p, u32x4 v) {
+#if BEVPOOL_PLANAR_NT
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
+template <bool kVec, int kIt>
+__global__ __launch_bounds__(kThreads) void planar_rows_kernel(
+    const float *__restrict__ src, int C, int64_t S, int64_t tiles_s, int64_t n_rows,
+    int64_t sbn, int64_t sc, float *__restrict__ rows) {
+  if constexpr (kVec) {
+    const int64_t bn = int64_t(blockIdx.x) / tiles_s;
+    const int64_t ts = int64_t(blockIdx.x) - bn * tiles_s;
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    const int64_t s0 = ts * 256 + w * 64 + (lane & 15) * 4;
+    if (s0 >= S) return;
+    const float *in = src + bn * sbn + s0;
+    u32x4 *out = reinterpret_cast<u32x4 *>(rows + (bn * S + s0) * C);
+    const int q = C / 4;  // 16-byte pieces per row
+    // all channels of these rows, 16 at a time (kIt passes with every load
+    // issued before the first store), so each row is completed by this wave
+    // within a few instructions
+    for (int cb = (lane >> 4) * 4; cb < C; cb += 16 * kIt) {
+      u32x4 a[kIt][4];
+#pragma unroll
+      for (int i = 0; i < kIt; ++i) {
+        const int c0 = cb + 16 * i < C ? cb + 16 * i : cb;  // past C: reload (not stored)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          a[i][k] = *reinterpret_cast<const u32x4 *>(in + int64_t(c0 + k) * sc);
       }
-      ctile[t * pitch + c] = v;
+#pragma unroll
+      for (int i = 0; i < kIt; ++i) {
+        if (cb + 16 * i < C) {
+          u32x4 *o = out + (cb + 16 * i) / 4;
+          store16(o, u32x4{a[i][0].x, a[i][1].x, a[i][2].x, a[i][3].x});
+          store16(o + q, u32x4{a[i][0].y, a[i][1].y, a[i][2].y, a[i][3].y});
+          store16(o + 2 * q, u32x4{a[i][0].z, a[i][1].z, a[i][2].z, a[i][3].z});
+          store16(o + 3 * q, u32x4{a[i][0].w, a[i][1].w, a[i][2].w, a[i][3].w});
+        }
+      }
     }
-    __syncthreads();
-    for (int i = tid; i < kCellTile * cb; i += kThreads) {
-      const int t = i / cb, c = i - t * cb;
-      if (pix0 + t < n_pix) rows[(pix0 + t) * C + c0 + c] = ctile[t * pitch + c];
+  } else {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n_rows * C) return;
+    const int64_t r = i / C;
+    const int c = int(i - r * C);
+    const int64_t bn = r / S, sp = r - bn * S;
+    rows[i] = src[bn * sbn + int64_t(c) * sc + sp];
+  }
+}
+
+// Backward of the op-level pooling into a planar gradient:
+// x_grad[bn, c, s] = g[rank[bn*S + s], c] (0 for dropped points), g the
+// cell-major rows of bev_to_rows_kernel.  Vector form (C, S, sbn, sc multiples
+// of 4, 16-byte aligned x_grad): a thread takes 4 consecutive points and walks
+// the channels 4 at a time: four 16-byte row loads (cache-resident rows), a
+// register transpose, four 16-byte stores along s (a wave writes 1 KB
+// contiguous per channel, non-temporal).  Blocks map XCD-contiguously.
+template <bool kVec, int kIt>
+__global__ __launch_bounds__(kThreads) void gather_planar_kernel(
+    const float *__restrict__ g, int C, const int32_t *__restrict__ rank, int64_t n_points,
+    int64_t S, int64_t sbn, int64_t sc, float *__restrict__ x_grad) {
+  if constexpr (kVec) {
+    const int64_t groups = n_points / 4;  // S % 4 == 0: a group never spans two bn
+    const int64_t gi = xcd_chunk(blockIdx.x, gridDim.x) * kThreads + threadIdx.x;
+    if (gi >= groups) return;
+    const int64_t p0 = gi * 4;
+    const u32x4 rk = *reinterpret_cast<const u32x4 *>(rank + p0);
+    const int r0 = int(rk.x), r1 = int(rk.y), r2 = int(rk.z), r3 = int(rk.w);
+    const u32x4 *g0 = reinterpret_cast<const u32x4 *>(g + int64_t(r0 >= 0 ? r0 : 0) * C);
+    const u32x4 *g1 = reinterpret_cast<const u32x4 *>(g + int64_t(r1 >= 0 ? r1 : 0) * C);
+    const u32x4 *g2 = reinterpret_cast<const u32x4 *>(g + int64_t(r2 >= 0 ? r2 : 0) * C);
+    const u32x4 *g3 = reinterpret_cast<const u32x4 *>(g + int64_t(r3 >= 0 ? r3 : 0) * C);
+    const uint32_t m0 = r0 >= 0 ? 0xFFFFFFFFu : 0u, m1 = r1 >= 0 ? 0xFFFFFFFFu : 0u;
+    const uint32_t m2 = r2 >= 0 ? 0xFFFFFFFFu : 0u, m3 = r3 >= 0 ? 0xFFFFFFFFu : 0u;
+    const int64_t bn = p0 / S, sp = p0 - bn * S;
+    float *out = x_grad + bn * sbn + sp;
+    const int nq = C / 4;
+    for (int qb = 0; qb < nq; qb += kIt) {
+      u32x4 a[kIt][4];
+#pragma unroll
+      for (int i = 0; i < kIt; ++i) {  // every row piece of kIt groups, then the stores
+        const int q = qb + i < nq ? qb + i : qb;
+        a[i][0] = g0[q] & m0;
+        a[i][1] = g1[q] & m1;
+        a[i][2] = g2[q] & m2;
+        a[i][3] = g3[q] & m3;
+      }
+#pragma unroll
+      for (int i = 0; i < kIt; ++i) {
+        if (qb + i < nq) {
+          float *o = out + int64_t(4 * (qb + i)) * sc;
+          __builtin_nontemporal_store(u32x4{a[i][0].x, a[i][1].x, a[i][2].x, a[i][3].x},
+                                      reinterpret_cast<u32x4 *>(o));
+          __builtin_nontemporal_store(u32x4{a[i][0].y, a[i][1].y, a[i][2].y, a[i][3].y},
+                                      reinterpret_cast<u32x4 *>(o + sc));
+          __builtin_nontemporal_store(u32x4{a[i][0].z, a[i][1].z, a[i][2].z, a[i][3].z},
+                                      reinterpret_cast<u32x4 *>(o + 2 * sc));
+          __builtin_nontemporal_store(u32x4{a[i][0].w, a[i][1].w, a[i][2].w, a[i][3].w},
+                                      reinterpret_cast<u32x4 *>(o + 3 * sc));
+        }
+      }
     }
-    __syncthreads();
+  } else {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n_points * C) return;
+    const int c = int(i / n_points);
+    const int64_t p = i - int64_t(c) * n_points;
+    const int r = rank[p];
+    const int64_t bn = p / S, sp = p - bn * S;
+    x_grad[bn * sbn + int64_t(c) * sc + sp] = r >= 0 ? g[int64_t(r) * C + c] : 0.0f;
   }
 }
 
@@ -1632,7 +1740,7 @@ constexpr int kDgPix = 16;  // pixels per depth_grad block (4 per wave)
 // sums are combined in row order at the end of the pixel.  The dot products
 // replace the ranks in LDS and, like the context sums, are written out
 // coalesced.  g: cell-major fp32 rows of the occupied cells; ctx:
-// channel-last rows (context_rows_kernel).  Blocks map XCD-contiguously, so
+// channel-last rows (planar_rows_kernel).  Blocks map XCD-contiguously, so
 // the cells of neighbouring pixels' rays meet in one L2.
 template <int kK, int kU>
 __global__ __launch_bounds__(kThreads) void depth_grad_kernel(
@@ -2249,20 +2357,85 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
                             out_stride_b, out_stride_c, out_stride_z, out, s);
 }
 
+int bevpool_planar_rows(const float *src, int64_t stride_bn, int64_t stride_c, int32_t BN,
+                        int32_t C, int64_t S, float *rows, void *stream) {
+  g_last_error.clear();
+  if (BN < 0 || C < 1 || S < 0) return fail(BEVPOOL_EINVAL, "bad planar shape");
+  const int64_t n_rows = int64_t(BN) * S;
+  if (n_rows == 0) return BEVPOOL_OK;
+  if (!src || !rows) return fail(BEVPOOL_EINVAL, "null argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool vec = C % 4 == 0 && S % 4 == 0 && stride_bn % 4 == 0 && stride_c % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(rows) % 16 == 0;
+  LaunchTimer t("planar_rows", s);
+  if (vec) {
+    const int64_t tiles_s = ceil_div(S, 256);
+    const int passes = (C + 15) / 16;  // 16-channel passes per thread
+#define BEVPOOL_PR(IT)                                                                         \
+  hipLaunchKernelGGL((planar_rows_kernel<true, IT>), dim3(unsigned(int64_t(BN) * tiles_s)),     \
+                     dim3(kThreads), 0, s, src, C, S, tiles_s, n_rows, stride_bn, stride_c, rows)
+    if (passes <= 1) BEVPOOL_PR(1);
+    else if (passes <= 2) BEVPOOL_PR(2);
+    else if (passes <= 3) BEVPOOL_PR(3);
+    else if (passes <= 5) BEVPOOL_PR(5);
+    else BEVPOOL_PR(4);
+#undef BEVPOOL_PR
+  } else {
+    hipLaunchKernelGGL((planar_rows_kernel<false, 1>),
+                       dim3(unsigned(ceil_div(n_rows * C, kThreads))), dim3(kThreads), 0, s, src,
+                       C, S, int64_t(0), n_rows, stride_bn, stride_c, rows);
+  }
+  return check_launch("planar_rows");
+}
+
 int bevpool_context_rows(const float *context, int64_t stride_bn, int64_t stride_c, int32_t BN,
                          int32_t C, int64_t HW, float *rows, void *stream) {
+  return bevpool_planar_rows(context, stride_bn, stride_c, BN, C, HW, rows, stream);
+}
+
+int bevpool_backward_planar(const float *grad, int64_t grad_stride_b, int64_t grad_stride_c,
+                            int64_t grad_stride_z, int32_t C, const int32_t *rank,
+                            int64_t n_points, const int32_t *cell_start,
+                            const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                            int64_t S, float *x_grad, int64_t x_stride_bn, int64_t x_stride_c,
+                            void *scratch, size_t scratch_bytes, void *stream) {
   g_last_error.clear();
-  if (BN < 0 || C < 1 || HW < 0) return fail(BEVPOOL_EINVAL, "bad context shape");
-  const int64_t n_pix = int64_t(BN) * HW;
-  if (n_pix == 0) return BEVPOOL_OK;
-  if (!context || !rows) return fail(BEVPOOL_EINVAL, "null argument");
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (n_batch < 1 || n_z < 1 || n_xy < 1) return fail(BEVPOOL_EINVAL, "bad grid");
+  const int64_t n_cells = int64_t(n_batch) * n_z * n_xy;
+  if (n_cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "too many cells");
+  if (S < 1 || n_points < 0 || n_points > int64_t(INT32_MAX) || n_points % S != 0)
+    return fail(BEVPOOL_EINVAL, "n_points must be a multiple of S");
+  if (n_points == 0) return BEVPOOL_OK;
+  if (!grad || !rank || !cell_start || !cell_end || !x_grad)
+    return fail(BEVPOOL_EINVAL, "null argument");
+  if (!scratch || scratch_bytes < bevpool_backward_scratch_bytes(n_cells, C, BEVPOOL_F32))
+    return fail(BEVPOOL_ESPACE, "backward scratch too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int CT = C < kTileChannels ? C : kTileChannels;
-  const size_t smem = size_t(kCellTile) * size_t(CT + 1) * sizeof(float);
-  LaunchTimer t("context_rows", s);
-  hipLaunchKernelGGL(context_rows_kernel, dim3(unsigned(ceil_div(n_pix, kCellTile))),
-                     dim3(kThreads), smem, s, context, C, HW, n_pix, stride_bn, stride_c, rows);
-  return check_launch("context_rows");
+  int st;
+  if ((st = launch_bev_to_rows(grad, 4, grad_stride_b, grad_stride_c, grad_stride_z, C,
+                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
+    return st;
+  const bool vec = C % 4 == 0 && S % 4 == 0 && x_stride_bn % 4 == 0 && x_stride_c % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(x_grad) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(rank) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(scratch) % 16 == 0;
+  const float *g = static_cast<const float *>(scratch);
+  LaunchTimer t("gather_planar", s);
+  if (vec) {
+    const unsigned grid = xcd_grid(ceil_div(n_points / 4, kThreads));
+#ifndef BEVPOOL_GP_IT
+#define BEVPOOL_GP_IT 2
+#endif
+    hipLaunchKernelGGL((gather_planar_kernel<true, BEVPOOL_GP_IT>), dim3(grid), dim3(kThreads),
+                       0, s, g, C, rank, n_points, S, x_stride_bn, x_stride_c, x_grad);
+  } else {
+    hipLaunchKernelGGL((gather_planar_kernel<false, 1>),
+                       dim3(unsigned(ceil_div(n_points * C, kThreads))), dim3(kThreads), 0, s, g,
+                       C, rank, n_points, S, x_stride_bn, x_stride_c, x_grad);
+  }
+  return check_launch("gather_planar");
 }
 
 int bevpool_forward_depth(const float *depth, const float *context_rows, int32_t C,

@@ -12,7 +12,8 @@ cameras, dense near the car, sparse far away):
 The camera rig: six cameras at yaw 0, +-55, +-110, 180 degrees, 1.5 m high,
 pinhole intrinsics with the principal point at the image centre.  Named
 cases follow the five benchmark configurations (det, seg, train, bf16,
-hires) plus a small ``tiny`` case for smoke tests.
+hires) plus a small ``tiny`` case for smoke tests and two cases with four
+height bins (``tiny_z4``, ``det_z4``).
 """
 from __future__ import annotations
 
@@ -53,6 +54,11 @@ CASES = {
     'hires': RigSpec(batch=2, image=(512, 1408), feature=(64, 176), focal=1120.0,
                      xbound=(-54.0, 54.0, 0.15), ybound=(-54.0, 54.0, 0.15),
                      oob_fraction=0.10, edge_points=64),
+    # several height bins (Z-collapse to C*Dz channels); points above/below drop
+    'tiny_z4': RigSpec(image=(64, 176), feature=(8, 22), focal=140.0, dbound=(1.0, 60.0, 2.0),
+                       xbound=(-54.0, 54.0, 1.2), ybound=(-54.0, 54.0, 1.2),
+                       zbound=(-3.0, 3.0, 1.5), channels=16, edge_points=8),
+    'det_z4': RigSpec(zbound=(-3.0, 3.0, 1.5)),
 }
 
 

@@ -18,9 +18,11 @@ flows to ``x`` only (the reference's ``.long()`` cuts it from the geometry),
 with zero rows for dropped points, as autograd of ``x[kept]`` gives.
 
 Like ``@force_fp32`` (``models/helper/amp.py:35-67``) the inputs are cast to
-fp32 first.  ``x`` may be any (B, N, D, fH, fW, C) view whose flattening to
-(N_all, C) has unit channel stride -- a channel-last producer costs no copy;
-otherwise it is copied once, as ``rearrange`` does at ``base.py:136``.
+fp32 first.  ``x`` may be any (B, N, D, fH, fW, C) view: a channel-last
+producer costs no copy; the reference's own view of channel-first storage
+(``depth_lss.py:94``) is transposed into rows by one kernel (the copy
+``base.py:136`` makes) and its gradient is written back channel-first without
+a copy; other views are copied once.
 """
 from __future__ import annotations
 
@@ -51,30 +53,63 @@ def host_grid(dx, bx, nx):
     return offset, dx32.numpy().astype(np.float32), nxl
 
 
+def planar_layout(x):
+    """(stride_bn, stride_c, S) if the (B, N, D, fH, fW, C) tensor ``x`` is a
+    view of planar storage, element (bn, c, s) at bn*stride_bn + c*stride_c + s
+    with S = D*fH*fW and unit stride along s -- the layout of the reference's
+    ``rearrange(x, '(b n) c d h w -> b n d h w c')`` (``depth_lss.py:94``);
+    else None."""
+    B, N, D, fH, fW, C = x.shape
+    st = x.stride()
+    S = D * fH * fW
+    if C < 2 or S < 2 or st[4] != 1 or st[3] != fW or st[2] != fH * fW or st[5] < S:
+        return None
+    if B == 1 or N == 1:
+        sbn = st[1] if B == 1 else st[0]
+    elif st[0] == N * st[1]:
+        sbn = st[1]
+    else:
+        return None
+    return sbn, st[5], S
+
+
 class _LSSBevPool(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, geom_feats, offset, dx, nx):
         B, N, D, fH, fW, C = x.shape
         X, Y, Z = nx
-        x2 = x.reshape(B * N * D * fH * fW, C)
-        if x2.stride(1) != 1 and x2.shape[0]:
-            x2 = x2.contiguous()
+        planar = planar_layout(x) if x.numel() else None
+        if planar is not None:
+            # channel-first storage: one transposing kernel instead of the
+            # reshape copy of base.py:136; the gradient goes back planar
+            sbn, sc, S = planar
+            x2 = P.planar_rows(x.as_strided((B * N, C, S), (sbn, sc, 1)))
+        else:
+            x2 = x.reshape(B * N * D * fH * fW, C)
+            if x2.stride(1) != 1 and x2.shape[0]:
+                x2 = x2.contiguous()
         idx = P.index_from_geom(geom_feats.reshape(-1, 3), B, offset, dx, nx)
         out = torch.empty((B, Z * C, X, Y), dtype=torch.float32, device=x.device)
         # element (b, c, z, xy) of the (B, C, Dz, H, W) pool at channel z*C + c
         P.forward(idx, x2, out, Z * C * X * Y, X * Y, C * X * Y)
         ctx.pool_index = idx
         ctx.x_shape = x.shape
+        ctx.planar = planar is not None
         return out
 
     @staticmethod
     def backward(ctx, g):
         idx = ctx.pool_index
-        C = ctx.x_shape[-1]
+        B, N, D, fH, fW, C = ctx.x_shape
         if g.dtype != torch.float32:
             g = g.float()
         if g.stride(3) != 1 or g.stride(2) != idx.W:
             g = g.contiguous()
+        if ctx.planar:
+            storage = torch.empty((B, N, C, D, fH, fW), dtype=torch.float32, device=g.device)
+            P.backward_planar(idx, g, C, g.stride(0), g.stride(1), C * g.stride(1),
+                              storage.view(B * N, C, D * fH * fW))
+            return storage.permute(0, 1, 3, 4, 5, 2), None, None, None, None
         x_grad = torch.empty(ctx.x_shape, dtype=torch.float32, device=g.device)
         P.backward(idx, g, C, g.stride(0), g.stride(1), C * g.stride(1),
                    x_grad.view(-1, C))

@@ -199,6 +199,37 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                      size_t scratch_bytes, void *stream);
 
 /*
+ * Planar (channel-first) camera features.  The reference's features are the
+ * view rearrange(x, '(b n) c d h w -> b n d h w c') of channel-first storage
+ * (models/vtransforms/depth_lss.py:94); base.py:136 then copies them into
+ * (N_all, C) rows with x.reshape.  A planar tensor (BN, C, S), S = D*fH*fW,
+ * has element (bn, c, s) at bn*stride_bn + c*stride_c + s; point p = bn*S + s.
+ */
+
+/*
+ * Planar (BN, C, S) fp32 -> rows [BN*S, C] fp32 (the copy of base.py:136,
+ * as one transposing kernel).  Any strides; the fast form needs C, S and both
+ * strides multiples of 4 and 16-byte aligned pointers.
+ */
+int bevpool_planar_rows(const float *src, int64_t stride_bn, int64_t stride_c, int32_t BN,
+                        int32_t C, int64_t S, float *rows, void *stream);
+
+/*
+ * Backward of the pooling straight into a planar fp32 gradient:
+ * x_grad[bn, c, s] = grad at the cell of point bn*S + s (0 for dropped
+ * points), i.e. the gradient autograd hands the channel-first producer
+ * through the rearrange view (bev_pool_triton.py:192 gather, then
+ * depth_lss.py:94 and base.py:136 backwards).  Arguments as bevpool_backward
+ * (fp32 grad) plus S and the x_grad strides; n_points = BN*S.
+ */
+int bevpool_backward_planar(const float *grad, int64_t grad_stride_b, int64_t grad_stride_c,
+                            int64_t grad_stride_z, int32_t C, const int32_t *rank,
+                            int64_t n_points, const int32_t *cell_start,
+                            const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
+                            int64_t S, float *x_grad, int64_t x_stride_bn, int64_t x_stride_c,
+                            void *scratch, size_t scratch_bytes, void *stream);
+
+/*
  * Depth-weighted (fused depth x context) pooling.  The reference builds the
  * camera features as the outer product x[bn, c, d, h, w] =
  * depth[bn, d, h, w] * context[bn, c, h, w] (models/vtransforms/depth_lss.py:
@@ -215,7 +246,8 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
  * Context (BN, C, HW) fp32, element (bn, c, hw) at bn*stride_bn + c*stride_c
  * + hw, to channel-last rows [BN*HW, C] (the layout the pooled rows are read
  * in).  Replaces the context operand of depth_lss.py:92 (x[:, D:D+C], a
- * channel-first slice of the depthnet output).
+ * channel-first slice of the depthnet output).  Same as bevpool_planar_rows
+ * with S = HW.
  */
 int bevpool_context_rows(const float *context, int64_t stride_bn, int64_t stride_c, int32_t BN,
                          int32_t C, int64_t HW, float *rows, void *stream);

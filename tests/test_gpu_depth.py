@@ -102,6 +102,11 @@ def test_depth_pool_train_batch4(pkg, cuda, synthetic):
     check_depth_pool(pkg, 'train', synthetic, cuda, seed=3)
 
 
+def test_depth_pool_height_bins(pkg, cuda, synthetic):
+    """Dz = 4: the fused path writes the (B, C*Dz, H, W) collapse directly."""
+    check_depth_pool(pkg, 'tiny_z4', synthetic, cuda)
+
+
 def test_depth_pool_hires_out_of_bounds_forward(pkg, cuda, synthetic):
     """720x720 grid, B=2, 10% of the points out of bounds (forward only: the
     float64 gradient oracle at 4.3 M points x 80 channels is left to the

@@ -103,6 +103,19 @@ def test_bf16_batch8_op_level(pkg, cuda, synthetic):
     assert_bit_equal(f.grad, ref.backward_gather(g, coords, *sizes), 'bf16 bwd (copy)')
 
 
+@pytest.mark.parametrize('name', ['tiny_z4', 'det_z4'])
+def test_lss_height_bins_z_collapse(pkg, cuda, synthetic, name):
+    """Dz = 4 height bins: the (B, C*Dz, H, W) output of base.py:163
+    (cat(unbind(2), 1): channel z*C + c) written directly, forward and
+    backward bit-exact; points above or below the bins are dropped."""
+    case = synthetic.make_case(name)
+    dx, bx, nx = grid_of(case)
+    assert int(nx[2]) == 4
+    oi = check_index(pkg, case, cuda)
+    assert 0 < int(oi.kept.sum()) < case.n_points
+    check_fwd_bwd(pkg, case, cuda)
+
+
 def test_lss_deterministic_and_stream(pkg, cuda, synthetic):
     case = synthetic.make_case('tiny')
     module = pkg.BevPoolTransform(case.xbound, case.ybound, case.zbound).to(cuda)
@@ -116,15 +129,57 @@ def test_lss_deterministic_and_stream(pkg, cuda, synthetic):
     assert torch.equal(a.cpu().view(torch.int32), b.cpu().view(torch.int32))
 
 
-def test_lss_channel_first_producer_view(pkg, cuda, synthetic):
-    """x given as the reference's view of channel-first storage
-    (depth_lss.py:94 rearrange) is copied once and pooled identically."""
-    case = synthetic.make_case('tiny')
-    B, N, D, fH, fW, C = case.x.shape
-    cf = case.x.permute(0, 1, 5, 2, 3, 4).contiguous()  # (B, N, C, D, fH, fW) storage
-    view = cf.to(cuda).permute(0, 1, 3, 4, 5, 2)  # (B, N, D, fH, fW, C) view
+def check_planar(pkg, cuda, case, storage, view_of, seed=8):
+    """Forward and backward through a channel-first (planar) view of
+    ``storage``, bit-exact against the oracle on the same values; the
+    gradient comes back in the planar layout."""
+    leaf = storage.to(cuda).requires_grad_(True)
+    view = view_of(leaf)
     assert not view.is_contiguous()
+    from bevfusion_triton_amd.vtransform import planar_layout
+
+    assert planar_layout(view) is not None
     module = pkg.BevPoolTransform(case.xbound, case.ybound, case.zbound).to(cuda)
     out = module.bev_pool(case.geom.to(cuda), view)
     dx, bx, nx = grid_of(case)
-    assert_bit_equal(out, ref.lss_bev_pool(case.geom, case.x, dx, bx, nx), 'channel-first view')
+    xr = view_of(storage).detach().clone().requires_grad_(True)
+    out_ref = ref.lss_bev_pool(case.geom, xr, dx, bx, nx)
+    assert_bit_equal(out, out_ref, f'{case.name} planar forward')
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(seed))
+    (out * g.to(cuda)).sum().backward()
+    (out_ref * g).sum().backward()
+    assert_bit_equal(view_of(leaf.grad), xr.grad, f'{case.name} planar backward')
+
+
+def test_lss_channel_first_producer_view(pkg, cuda, synthetic):
+    """x given as the reference's view of channel-first storage
+    (depth_lss.py:94 rearrange) is transposed by one kernel and its gradient
+    written back channel-first; both bit-exact."""
+    case = synthetic.make_case('tiny')
+    cf = case.x.permute(0, 1, 5, 2, 3, 4).contiguous()  # (B, N, C, D, fH, fW) storage
+    check_planar(pkg, cuda, case, cf, lambda t: t.permute(0, 1, 3, 4, 5, 2))
+
+
+def test_lss_channel_first_det(pkg, cuda, synthetic):
+    """The planar path at the det shape (vector kernels)."""
+    case = synthetic.make_case('det')
+    cf = case.x.permute(0, 1, 5, 2, 3, 4).contiguous()
+    check_planar(pkg, cuda, case, cf, lambda t: t.permute(0, 1, 3, 4, 5, 2))
+
+
+def test_lss_channel_first_channel_slice(pkg, cuda, synthetic):
+    """A planar view whose batch stride exceeds C*S (a channel slice of a
+    wider tensor, as depth_lss.py:92 slices the depth-net output)."""
+    case = synthetic.make_case('tiny')
+    B, N, D, fH, fW, C = case.x.shape
+    wide = torch.randn(B, N, C + 5, D, fH, fW, generator=torch.Generator().manual_seed(2))
+    wide[:, :, 2:2 + C] = case.x.permute(0, 1, 5, 2, 3, 4)
+    check_planar(pkg, cuda, case, wide, lambda t: t[:, :, 2:2 + C].permute(0, 1, 3, 4, 5, 2))
+
+
+def test_lss_channel_first_odd_channels(pkg, cuda, synthetic):
+    """C = 6 takes the element-wise planar kernels (no 16-byte form)."""
+    case = synthetic.make_case('tiny', features=False)
+    B, N, D, fH, fW = case.geom.shape[:5]
+    cf = torch.randn(B, N, 6, D, fH, fW, generator=torch.Generator().manual_seed(4))
+    check_planar(pkg, cuda, case, cf, lambda t: t.permute(0, 1, 3, 4, 5, 2))
