@@ -279,6 +279,8 @@ def main():
     fused = depth_fused(pkg, geom, module, spec, dev)
     # secondary figure: channel-first (planar) features, the reference's layout
     planar = channel_first(pkg, geom, module, x.detach(), g, dev)
+    # secondary figure: geometry from camera matrices fused into the index
+    cams = camera_index(pkg, spec, module, x.detach(), dev)
 
     # per-kernel durations from HIP events on the launch stream
     log(f'[bench] per-kernel timing over {args.profile_steps} steps')
@@ -373,6 +375,7 @@ def main():
         'op_level': op,
         'depth_fused': fused,
         'channel_first': planar,
+        'camera_index': cams,
         'kernels': kernels,
         'calibration': cal,
     }
@@ -505,6 +508,64 @@ def channel_first(pkg, geom, module, x, g, dev):
                                                    1)}
     del storage
     return res
+
+
+def camera_index(pkg, spec, module, x, dev):
+    """Index stage from camera matrices (base.py:82-126 fused into the
+    quantisation, lss_index_cameras) against the reference's get_geometry in
+    torch on the same GPU followed by this library's index stage; and a
+    static-camera forward (cached index, inference).  HIP events."""
+    from bevfusion_triton_amd import synthetic
+    from bevfusion_triton_amd import _pipeline as P
+
+    inp = synthetic.camera_inputs(spec, seed=7, augment=True)
+    gi = {k: (v.to(dev) if v is not None else None) for k, v in inp.items()}
+    off, d, n = module.grid()
+
+    def torch_geometry():
+        # base.py:82-126 as the reference runs it (torch ops on the device)
+        B, N, _ = gi['camera2lidar_trans'].shape
+        pts = gi['frustum'] - gi['post_trans'].view(B, N, 1, 1, 1, 3)
+        pts = gi['post_rots'].transpose(-1, -2).reshape(B, N, 1, 1, 1, 3, 3).matmul(
+            pts.unsqueeze(-1))
+        pts = torch.cat((pts[..., :2, :] * pts[..., 2:3, :], pts[..., 2:3, :]), 5)
+        comb = torch.linalg.solve(gi['intrins'].transpose(-1, -2),
+                                  gi['camera2lidar_rots'].transpose(-1, -2)).transpose(-1, -2)
+        pts = comb.reshape(B, N, 1, 1, 1, 3, 3).matmul(pts).squeeze(-1)
+        pts = pts + gi['camera2lidar_trans'].view(B, N, 1, 1, 1, 3)
+        pts = gi['extra_rots'].view(B, 1, 1, 1, 1, 3, 3).matmul(pts.unsqueeze(-1)).squeeze(-1)
+        return pts + gi['extra_trans'].view(B, 1, 1, 1, 1, 3)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    fused_us = timed(lambda: module.index_cameras(**gi), 20)
+    geo_us = timed(torch_geometry, 3)
+    geo = torch_geometry()
+    idx_us = timed(lambda: P.index_from_geom(geo.reshape(-1, 3), spec.batch, off, d, n), 20)
+    cached = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound, cache_index=True).to(dev)
+    with torch.no_grad():
+        cold_us = timed(lambda: module.bev_pool(module.index_cameras(**gi), x), 20)
+        cached.index_cameras(**gi)
+        warm_us = timed(lambda: cached.bev_pool(cached.index_cameras(**gi), x), 20)
+    n_all = x[..., 0].numel()
+    return {'what': 'index stage from camera matrices: fused (lss_index_cameras) vs torch '
+                    'get_geometry on the GPU + index_from_geom; forward-only with the index '
+                    'recomputed vs cached (static cameras)',
+            'fused_index_us': round(fused_us, 1),
+            'torch_get_geometry_us': round(geo_us, 1),
+            'index_from_geom_us': round(idx_us, 1),
+            'forward_recomputed_us': round(cold_us, 1),
+            'forward_cached_index_us': round(warm_us, 1),
+            'forward_cached_points_per_s': round(n_all / (warm_us * 1e-6), 1)}
 
 
 def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):

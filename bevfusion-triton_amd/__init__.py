@@ -9,6 +9,8 @@ ziyangyeh/bevfusion-triton behind the reference's own Python surface:
   lss_bev_pool                              the same as a function
   lss_bev_pool_depth                        the same fused with depth_lss.py:91-94's
                                             depth (x) context product
+  lss_index_cameras / CameraIndex           base.py:82-126 get_geometry fused into the
+                                            quantisation (cacheable for static cameras)
 
 The kernels live in ``csrc/bevpool.hip`` and are reached through the C ABI of
 ``include/bevpool.h`` (``libbevpool_amd.so``, loaded by ``_lib``).  There is no
@@ -19,20 +21,23 @@ The directory name is not a Python identifier; load it with
 """
 from ._lib import BevPoolError, LibraryNotBuilt, library
 from .bev_pool import BevPoolFunction, BevPoolIndexExport, bev_pool
-from .vtransform import (BevPoolTransform, LSSIndexExport, gen_dx_bx, host_grid, lss_bev_pool,
-                         lss_bev_pool_depth)
+from .vtransform import (BevPoolTransform, CameraIndex, LSSIndexExport, create_frustum, gen_dx_bx, host_grid, lss_bev_pool, lss_bev_pool_depth,
+                         lss_index_cameras)
 
 __all__ = [
     'BevPoolError',
     'BevPoolFunction',
     'BevPoolIndexExport',
     'BevPoolTransform',
+    'CameraIndex',
     'LSSIndexExport',
     'LibraryNotBuilt',
     'bev_pool',
+    'create_frustum',
     'gen_dx_bx',
     'host_grid',
     'library',
     'lss_bev_pool',
     'lss_bev_pool_depth',
+    'lss_index_cameras',
 ]

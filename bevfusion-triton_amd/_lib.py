@@ -49,6 +49,11 @@ _SIGNATURES = {
         [_vp, _i64, _i64, _i64, _i32, _f3, _f3, _i3, _vp, _vp, _vp, _sz, _vp],
         ctypes.c_int,
     ),
+    'bevpool_quantize_cameras': (
+        [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f3, _f3, _i3,
+         _vp, _vp, _vp, _sz, _vp],
+        ctypes.c_int,
+    ),
     'bevpool_coord_ranks': (
         [_vp, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
         ctypes.c_int,

@@ -108,6 +108,49 @@ def index_from_geom(geom2d, B: int, offset, dx, nx) -> PoolIndex:
     return idx
 
 
+def index_from_cameras(frustum, mats, B: int, N: int, offset, dx, nx) -> PoolIndex:
+    """As :func:`index_from_geom` with the geometry computed inside the
+    quantisation from the frustum (D, fH, fW, 3) and the camera matrices
+    ``mats`` = (rots, trans, intrins, post_rots, post_trans, extra_rots,
+    extra_trans) (see ``bevpool_quantize_cameras``; the extras may be None)."""
+    require_gpu(frustum, *[m for m in mats if m is not None])
+    D, fH, fW, three = frustum.shape
+    if three != 3:
+        raise ValueError('frustum must be (D, fH, fW, 3)')
+    frustum = frustum.float().contiguous()
+    shapes = ((B * N, 3, 3), (B * N, 3), (B * N, 3, 3), (B * N, 3, 3), (B * N, 3), (B, 3, 3),
+              (B, 3))
+    flat = []
+    for m, shp in zip(mats, shapes):
+        if m is None:
+            flat.append(None)
+            continue
+        m = m.float().reshape(shp).contiguous()
+        flat.append(m)
+    if any(m is None for m in flat[:5]):
+        raise ValueError('rots, trans, intrins, post_rots and post_trans are required')
+    nx = [int(v) for v in nx]
+    n_points = B * N * D * fH * fW
+    _check_sizes(n_points, B * nx[0] * nx[1] * nx[2])
+    idx = PoolIndex(n_points, B, nx[2], nx[0], nx[1], frustum.device)
+    ws = idx.workspace()
+    stream = L.stream_handle(frustum.device)
+    lib = L.library()
+    off = np.asarray(offset, dtype=np.float32)
+    d = np.asarray(dx, dtype=np.float32)
+    with torch.cuda.device(frustum.device):
+        L.check(
+            lib.bevpool_quantize_cameras(
+                L.ptr(frustum), D, fH, fW, *[L.ptr(m) for m in flat], N, B,
+                L._f3(*[float(v) for v in off]), L._f3(*[float(v) for v in d]), L._i3(*nx),
+                L.ptr(idx.rank), L.ptr(idx.meta), L.ptr(ws), ws.numel(), stream,
+            ),
+            'bevpool_quantize_cameras',
+        )
+        _sort(idx, ws, stream)
+    return idx
+
+
 def _quantize(lib, geom2d, n_points, B, off, d, nx, idx, ws, stream):
     L.check(
         lib.bevpool_quantize_geom(

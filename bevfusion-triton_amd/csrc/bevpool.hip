@@ -370,6 +370,142 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
   for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
 }
 
+// ---- geometry from camera matrices, fused with the quantisation -----------
+//
+// models/vtransforms/base.py:82-126 (get_geometry) per point, in fp32 with
+// every product and sum rounded separately (no contraction), each 3x3
+// product summed left to right:
+//   a = frustum[d, h, w] - post_trans          (base.py:95)
+//   b = post_rots^T a                           (:96-98)
+//   c = (b0 b2, b1 b2, b2)                      (:100-106)
+//   g = combine c + camera2lidar_trans          (:107-112)
+//   g = extra_rots g + extra_trans              (:114-123, when given)
+// then quantize_point as for a geometry tensor.  combine = rots inv(intrins)
+// (the reference's linalg.solve) is formed in double from the adjugate of
+// intrins and rounded to fp32 once.  Per camera the kernel works from a
+// 24-float table: post_rots^T (9, row-major), post_trans (3), combine (9),
+// camera2lidar_trans (3); per batch a 12-float table: extra_rots (9),
+// extra_trans (3).
+constexpr int kCamFloats = 24;
+constexpr int kBatchFloats = 12;
+constexpr int kCamSlots = 16;  // cameras a block stages in LDS
+
+struct CameraMats {  // fp32, row-major, contiguous per camera / batch
+  const float *rots, *trans, *intrins, *post_rots, *post_trans;  // [B*N][9|3]
+  const float *extra_rots, *extra_trans;                         // [B][9|3] or null
+  int n_per_batch;                                               // N
+  __device__ __forceinline__ bool has_extra() const { return extra_rots || extra_trans; }
+};
+
+__device__ void camera_table(const CameraMats &m, uint32_t cam, float *__restrict__ t) {
+  const float *R = m.rots + int64_t(cam) * 9, *K = m.intrins + int64_t(cam) * 9;
+  const float *PR = m.post_rots + int64_t(cam) * 9;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) t[3 * i + j] = PR[3 * j + i];  // post_rots^T
+  for (int i = 0; i < 3; ++i) t[9 + i] = m.post_trans[int64_t(cam) * 3 + i];
+  double k[9];
+  for (int i = 0; i < 9; ++i) k[i] = double(K[i]);
+  const double c00 = k[4] * k[8] - k[5] * k[7], c01 = k[5] * k[6] - k[3] * k[8];
+  const double c02 = k[3] * k[7] - k[4] * k[6];
+  const double det = k[0] * c00 + k[1] * c01 + k[2] * c02;
+  double inv[9] = {c00, k[2] * k[7] - k[1] * k[8], k[1] * k[5] - k[2] * k[4],
+                   c01, k[0] * k[8] - k[2] * k[6], k[2] * k[3] - k[0] * k[5],
+                   c02, k[1] * k[6] - k[0] * k[7], k[0] * k[4] - k[1] * k[3]};
+  for (int i = 0; i < 9; ++i) inv[i] /= det;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      double v = 0.0;
+      for (int q = 0; q < 3; ++q) v += double(R[3 * i + q]) * inv[3 * q + j];
+      t[12 + 3 * i + j] = float(v);
+    }
+  for (int i = 0; i < 3; ++i) t[21 + i] = m.trans[int64_t(cam) * 3 + i];
+}
+
+__device__ void batch_table(const CameraMats &m, uint32_t b, float *__restrict__ t) {
+  for (int i = 0; i < 9; ++i)
+    t[i] = m.extra_rots ? m.extra_rots[int64_t(b) * 9 + i] : (i % 4 == 0 ? 1.0f : 0.0f);
+  for (int i = 0; i < 3; ++i) t[9 + i] = m.extra_trans ? m.extra_trans[int64_t(b) * 3 + i] : 0.0f;
+}
+
+__device__ __forceinline__ void frustum_point(const float *__restrict__ c,
+                                              const float *__restrict__ e, float fx, float fy,
+                                              float fz, float &gx, float &gy, float &gz) {
+  const float a0 = fx - c[9], a1 = fy - c[10], a2 = fz - c[11];
+  const float b0 = (c[0] * a0 + c[1] * a1) + c[2] * a2;
+  const float b1 = (c[3] * a0 + c[4] * a1) + c[5] * a2;
+  const float b2 = (c[6] * a0 + c[7] * a1) + c[8] * a2;
+  const float c0 = b0 * b2, c1 = b1 * b2;
+  gx = ((c[12] * c0 + c[13] * c1) + c[14] * b2) + c[21];
+  gy = ((c[15] * c0 + c[16] * c1) + c[17] * b2) + c[22];
+  gz = ((c[18] * c0 + c[19] * c1) + c[20] * b2) + c[23];
+  if (e) {
+    const float h0 = ((e[0] * gx + e[1] * gy) + e[2] * gz) + e[9];
+    const float h1 = ((e[3] * gx + e[4] * gy) + e[5] * gz) + e[10];
+    const float h2 = ((e[6] * gx + e[7] * gy) + e[8] * gz) + e[11];
+    gx = h0;
+    gy = h1;
+    gz = h2;
+  }
+}
+
+// Point p = cam * DHW + f (cam = b*N + n, f = (d*fH + h)*fW + w); frustum
+// fp32 (D, fH, fW, 3) contiguous.  A block takes kSortTile consecutive points
+// (as quantize_geom_kernel, so the pass-0 histograms line up); its first
+// threads build the tables of the cameras it spans in LDS.  A block spanning
+// more than kCamSlots cameras (frustums under ~140 points) builds each
+// point's table in registers instead.
+__global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
+    const float *__restrict__ frustum, int64_t n_points, uint32_t dhw, CameraMats cm, float o0,
+    float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
+    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits,
+    int32_t *__restrict__ meta) {
+  __shared__ int cnt[kMaxRadix];
+  __shared__ float lcam[kCamSlots][kCamFloats];
+  __shared__ float lbat[kCamSlots][kBatchFloats];
+  if (blockIdx.x == 0 && threadIdx.x < BEVPOOL_META_LEN)
+    meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
+  if (int(blockIdx.x) >= nblocks) return;
+  const int R = 1 << bits;
+  const unsigned mask = unsigned(R - 1);
+  for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
+  const uint32_t n = uint32_t(n_points);
+  const uint32_t base = uint32_t(blockIdx.x) * kSortTile;
+  const uint32_t last = (base + kSortTile < n ? base + kSortTile : n) - 1;
+  const uint32_t cam_lo = base / dhw, cam_hi = last / dhw;
+  const bool staged = cam_hi - cam_lo < uint32_t(kCamSlots);
+  const bool extra = cm.has_extra();
+  const uint32_t ppb = dhw * uint32_t(cm.n_per_batch);  // points per batch
+  if (staged && threadIdx.x <= cam_hi - cam_lo) {
+    const uint32_t cam = cam_lo + threadIdx.x;
+    camera_table(cm, cam, lcam[threadIdx.x]);
+    if (extra) batch_table(cm, cam / uint32_t(cm.n_per_batch), lbat[threadIdx.x]);
+  }
+  __syncthreads();
+  for (int k = 0; k < kItems; ++k) {
+    const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
+    int r = -1;
+    if (p < n) {
+      const uint32_t cam = p / dhw, f = p - cam * dhw;
+      const float *fr = frustum + int64_t(f) * 3;
+      float gx, gy, gz;
+      if (staged) {
+        frustum_point(lcam[cam - cam_lo], extra ? lbat[cam - cam_lo] : nullptr, fr[0], fr[1],
+                      fr[2], gx, gy, gz);
+      } else {
+        float ct[kCamFloats], bt[kBatchFloats];
+        camera_table(cm, cam, ct);
+        if (extra) batch_table(cm, cam / uint32_t(cm.n_per_batch), bt);
+        frustum_point(ct, extra ? bt : nullptr, fr[0], fr[1], fr[2], gx, gy, gz);
+      }
+      r = quantize_point(gx, gy, gz, p, ppb, o0, o1, o2, d0, d1, d2, n0, n1, n2);
+      if (r >= 0) atomicAdd(&cnt[unsigned(r) & mask], 1);
+      rank[p] = r;
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+}
+
 // ops/bev_pool/src/bev_pool_triton.py:34-39 in int64 (wrapping) arithmetic.
 template <typename TC>
 __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
@@ -2145,6 +2281,39 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
 #undef BEVPOOL_QUANT
   }
   return check_launch("quantize_geom");
+}
+
+int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_t fW,
+                             const float *rots, const float *trans, const float *intrins,
+                             const float *post_rots, const float *post_trans,
+                             const float *extra_rots, const float *extra_trans,
+                             int32_t n_cams_per_batch, int32_t n_batch, const float offset[3],
+                             const float dx[3], const int32_t nx[3], int32_t *rank,
+                             int32_t *meta, void *workspace, size_t workspace_bytes,
+                             void *stream) {
+  g_last_error.clear();
+  if (!offset || !dx || !nx) return fail(BEVPOOL_EINVAL, "null offset/dx/nx");
+  if (n_batch < 1 || n_cams_per_batch < 1 || D < 1 || fH < 1 || fW < 1)
+    return fail(BEVPOOL_EINVAL, "bad frustum/camera sizes");
+  if (nx[0] < 1 || nx[1] < 1 || nx[2] < 1) return fail(BEVPOOL_EINVAL, "bad grid");
+  const int64_t dhw = int64_t(D) * fH * fW;
+  const int64_t n_points = dhw * n_cams_per_batch * n_batch;
+  const int64_t n_cells = int64_t(n_batch) * nx[0] * nx[1] * nx[2];
+  int st = check_index_args(n_points, n_cells, rank, meta, workspace, workspace_bytes);
+  if (st) return st;
+  if (!frustum || !rots || !trans || !intrins || !post_rots || !post_trans)
+    return fail(BEVPOOL_EINVAL, "null frustum/camera matrices");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const IndexLayout L = index_layout(n_points);
+  const DigitPlan plan = plan_digits(n_cells);
+  const CameraMats cm{rots, trans, intrins, post_rots, post_trans, extra_rots, extra_trans,
+                      n_cams_per_batch};
+  LaunchTimer t("quantize_cameras", s);
+  hipLaunchKernelGGL(quantize_frustum_kernel, dim3(unsigned(L.sort_blocks)), dim3(kThreads), 0, s,
+                     frustum, n_points, uint32_t(dhw), cm, offset[0], offset[1], offset[2],
+                     dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,
+                     at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0], meta);
+  return check_launch("quantize_cameras");
 }
 
 int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_points,

@@ -108,6 +108,45 @@ def get_geometry(frustum, rots, trans, intrins):
     return out + trans.reshape(B, N, 1, 1, 1, 3)
 
 
+def camera_inputs(spec: RigSpec, seed: int = 1, augment: bool = True) -> dict:
+    """The arguments of ``get_geometry`` (``base.py:82-126``) for the rig:
+    frustum, camera2lidar rotations/translations, intrinsics and, with
+    ``augment``, an image augmentation per camera (post_rots = scale s in
+    [0.95, 1.05] times a rotation in +-5 degrees, post_trans a crop offset
+    of up to 8 px) and a lidar augmentation per sample (extra_rots a yaw in
+    +-10 degrees, extra_trans up to 0.5 m); identity/zero otherwise."""
+    gen = torch.Generator().manual_seed(seed)
+    frustum = create_frustum(spec.image, spec.feature, spec.dbound)
+    rots, trans, intrins = camera_rig(spec, gen)
+    B, N = spec.batch, len(YAWS_DEG)
+    out = {'frustum': frustum, 'camera2lidar_rots': rots, 'camera2lidar_trans': trans,
+           'intrins': intrins}
+    if augment:
+        s = 0.95 + 0.1 * torch.rand(B, N, generator=gen)
+        th = (torch.rand(B, N, generator=gen) * 2 - 1) * (5.0 * math.pi / 180.0)
+        pr = torch.zeros(B, N, 3, 3)
+        pr[..., 0, 0] = s * torch.cos(th)
+        pr[..., 0, 1] = -s * torch.sin(th)
+        pr[..., 1, 0] = s * torch.sin(th)
+        pr[..., 1, 1] = s * torch.cos(th)
+        pr[..., 2, 2] = 1.0
+        pt = torch.zeros(B, N, 3)
+        pt[..., :2] = (torch.rand(B, N, 2, generator=gen) * 2 - 1) * 8.0
+        yaw = (torch.rand(B, generator=gen) * 2 - 1) * (10.0 * math.pi / 180.0)
+        er = torch.zeros(B, 3, 3)
+        er[:, 0, 0] = torch.cos(yaw)
+        er[:, 0, 1] = -torch.sin(yaw)
+        er[:, 1, 0] = torch.sin(yaw)
+        er[:, 1, 1] = torch.cos(yaw)
+        er[:, 2, 2] = 1.0
+        et = (torch.rand(B, 3, generator=gen) * 2 - 1) * 0.5
+        out.update(post_rots=pr, post_trans=pt, extra_rots=er, extra_trans=et)
+    else:
+        out.update(post_rots=torch.eye(3).repeat(B, N, 1, 1), post_trans=torch.zeros(B, N, 3),
+                   extra_rots=None, extra_trans=None)
+    return out
+
+
 @dataclass
 class Case:
     name: str

@@ -26,6 +26,8 @@ a copy; other views are copied once.
 """
 from __future__ import annotations
 
+import weakref
+
 import numpy as np
 import torch
 from torch import nn
@@ -75,7 +77,7 @@ def planar_layout(x):
 
 class _LSSBevPool(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, geom_feats, offset, dx, nx):
+    def forward(ctx, x, geom_feats, offset, dx, nx, index=None):
         B, N, D, fH, fW, C = x.shape
         X, Y, Z = nx
         planar = planar_layout(x) if x.numel() else None
@@ -88,7 +90,10 @@ class _LSSBevPool(torch.autograd.Function):
             x2 = x.reshape(B * N * D * fH * fW, C)
             if x2.stride(1) != 1 and x2.shape[0]:
                 x2 = x2.contiguous()
-        idx = P.index_from_geom(geom_feats.reshape(-1, 3), B, offset, dx, nx)
+        if index is None:
+            idx = P.index_from_geom(geom_feats.reshape(-1, 3), B, offset, dx, nx)
+        else:
+            idx = index
         out = torch.empty((B, Z * C, X, Y), dtype=torch.float32, device=x.device)
         # element (b, c, z, xy) of the (B, C, Dz, H, W) pool at channel z*C + c
         P.forward(idx, x2, out, Z * C * X * Y, X * Y, C * X * Y)
@@ -109,11 +114,11 @@ class _LSSBevPool(torch.autograd.Function):
             storage = torch.empty((B, N, C, D, fH, fW), dtype=torch.float32, device=g.device)
             P.backward_planar(idx, g, C, g.stride(0), g.stride(1), C * g.stride(1),
                               storage.view(B * N, C, D * fH * fW))
-            return storage.permute(0, 1, 3, 4, 5, 2), None, None, None, None
+            return storage.permute(0, 1, 3, 4, 5, 2), None, None, None, None, None
         x_grad = torch.empty(ctx.x_shape, dtype=torch.float32, device=g.device)
         P.backward(idx, g, C, g.stride(0), g.stride(1), C * g.stride(1),
                    x_grad.view(-1, C))
-        return x_grad, None, None, None, None
+        return x_grad, None, None, None, None, None
 
 
 def lss_bev_pool(geom_feats, x, dx, bx, nx, *, grid=None):
@@ -122,12 +127,21 @@ def lss_bev_pool(geom_feats, x, dx, bx, nx, *, grid=None):
     geom_feats (B, N, D, fH, fW, 3), x (B, N, D, fH, fW, C) -> (B, C*Dz, H, W)
     fp32.  ``grid`` may pass a precomputed :func:`host_grid` triple to avoid
     reading device-resident dx/bx/nx back to the host on every call.
+    ``geom_feats`` may instead be a :class:`CameraIndex` (the index stage
+    computed from camera matrices by :func:`lss_index_cameras`).
     """
-    P.require_gpu(geom_feats, x)
     if torch.is_floating_point(x):
         x = x.float()
+    if x.dim() != 6:
+        raise ValueError('expected x (B, N, D, H, W, C)')
+    if isinstance(geom_feats, CameraIndex):
+        P.require_gpu(x)
+        geom_feats.check(x.shape[:5], grid)
+        offset, d, n = geom_feats.grid
+        return _LSSBevPool.apply(x, None, offset, d, tuple(n), geom_feats.index)
+    P.require_gpu(geom_feats, x)
     geom_feats = geom_feats.float()
-    if x.dim() != 6 or geom_feats.dim() != 6 or geom_feats.shape[-1] != 3:
+    if geom_feats.dim() != 6 or geom_feats.shape[-1] != 3:
         raise ValueError('expected geom_feats (B, N, D, H, W, 3) and x (B, N, D, H, W, C)')
     if geom_feats.shape[:5] != x.shape[:5]:
         raise ValueError('geom_feats and x must agree on (B, N, D, H, W)')
@@ -140,14 +154,17 @@ class _LSSBevPoolDepth(torch.autograd.Function):
     it: point p = (bn*D + d)*HW + hw carries depth[bn, d, hw] * context[bn, :, hw]."""
 
     @staticmethod
-    def forward(ctx, depth, context, geom_feats, B, offset, dx, nx):
+    def forward(ctx, depth, context, geom_feats, B, offset, dx, nx, index=None):
         BN, D, fH, fW = depth.shape
         C = context.shape[1]
         HW = fH * fW
         X, Y, Z = nx
         depth_flat = depth.contiguous().view(-1)
         rows = P.context_rows(context.reshape(BN, C, HW))
-        idx = P.index_from_geom(geom_feats.reshape(-1, 3), B, offset, dx, nx)
+        if index is None:
+            idx = P.index_from_geom(geom_feats.reshape(-1, 3), B, offset, dx, nx)
+        else:
+            idx = index
         out = torch.empty((B, Z * C, X, Y), dtype=torch.float32, device=depth.device)
         P.forward_depth(idx, depth_flat, rows, D, HW, out, Z * C * X * Y, X * Y, C * X * Y)
         ctx.pool_index = idx
@@ -168,7 +185,7 @@ class _LSSBevPoolDepth(torch.autograd.Function):
         grad_context = torch.empty((BN, C, fH, fW), dtype=torch.float32, device=g.device)
         P.backward_depth(idx, g, C, g.stride(0), g.stride(1), C * g.stride(1), depth_flat, rows,
                          D, fH * fW, grad_depth.view(-1), grad_context.view(BN, C, fH * fW))
-        return grad_depth, grad_context, None, None, None, None, None
+        return grad_depth, grad_context, None, None, None, None, None, None
 
 
 def lss_bev_pool_depth(geom_feats, depth, context, dx, bx, nx, *, grid=None):
@@ -184,26 +201,92 @@ def lss_bev_pool_depth(geom_feats, depth, context, dx, bx, nx, *, grid=None):
     context.  Channel counts the fused kernels do not take (C not a multiple
     of 4, or C > 256) pool the product formed on the GPU instead.
     """
-    P.require_gpu(geom_feats, depth, context)
-    if depth.dim() != 4 or context.dim() != 4 or geom_feats.dim() != 6 \
-            or geom_feats.shape[-1] != 3:
-        raise ValueError('expected geom_feats (B, N, D, H, W, 3), depth (B*N, D, H, W) and '
-                         'context (B*N, C, H, W)')
-    B, N, D, fH, fW = geom_feats.shape[:5]
+    camera_index = geom_feats if isinstance(geom_feats, CameraIndex) else None
+    if camera_index is not None:
+        P.require_gpu(depth, context)
+        shape = camera_index.shape
+    else:
+        P.require_gpu(geom_feats, depth, context)
+        if geom_feats.dim() != 6 or geom_feats.shape[-1] != 3:
+            raise ValueError('expected geom_feats (B, N, D, H, W, 3)')
+        shape = tuple(geom_feats.shape[:5])
+    if depth.dim() != 4 or context.dim() != 4:
+        raise ValueError('expected depth (B*N, D, H, W) and context (B*N, C, H, W)')
+    B, N, D, fH, fW = shape
     if tuple(depth.shape) != (B * N, D, fH, fW):
         raise ValueError('depth must be (B*N, D, H, W) matching geom_feats')
     if context.shape[0] != B * N or tuple(context.shape[2:]) != (fH, fW):
         raise ValueError('context must be (B*N, C, H, W) matching geom_feats')
     depth = depth.float()
     context = context.float()
-    geom_feats = geom_feats.float()
     C = context.shape[1]
-    offset, d, n = grid if grid is not None else host_grid(dx, bx, nx)
+    if camera_index is not None:
+        camera_index.check(shape, grid)
+        offset, d, n = camera_index.grid
+        geom_feats, index = None, camera_index.index
+    else:
+        geom_feats = geom_feats.float()
+        offset, d, n = grid if grid is not None else host_grid(dx, bx, nx)
+        index = None
     if C % 4 != 0 or C > 256 or C == 0:
         x = depth.unsqueeze(1) * context.unsqueeze(2)  # (BN, C, D, fH, fW)
         x = x.permute(0, 2, 3, 4, 1).reshape(B, N, D, fH, fW, C)
-        return _LSSBevPool.apply(x, geom_feats, offset, d, tuple(n))
-    return _LSSBevPoolDepth.apply(depth, context, geom_feats, B, offset, d, tuple(n))
+        return _LSSBevPool.apply(x, geom_feats, offset, d, tuple(n), index)
+    return _LSSBevPoolDepth.apply(depth, context, geom_feats, B, offset, d, tuple(n), index)
+
+
+def create_frustum(image_size, feature_size, dbound):
+    """``base.py:67-80``: (D, fH, fW, 3) fp32 of (u, v, depth) -- image
+    columns/rows by ``linspace`` over the feature grid, depths by ``arange``."""
+    iH, iW = image_size
+    fH, fW = feature_size
+    ds = torch.arange(*dbound, dtype=torch.float).view(-1, 1, 1).expand(-1, fH, fW)
+    D = ds.shape[0]
+    xs = torch.linspace(0, iW - 1, fW, dtype=torch.float).view(1, 1, fW).expand(D, fH, fW)
+    ys = torch.linspace(0, iH - 1, fH, dtype=torch.float).view(1, fH, 1).expand(D, fH, fW)
+    return torch.stack((xs, ys, ds), -1)
+
+
+class CameraIndex:
+    """The index stage of one frustum (ranks, sorted keys, cell ranges),
+    computed from camera matrices by :func:`lss_index_cameras`.  Pass it to
+    :func:`lss_bev_pool`, :func:`lss_bev_pool_depth` or the
+    :class:`BevPoolTransform` methods in place of ``geom_feats``; it can be
+    reused for as long as the cameras are unchanged."""
+
+    def __init__(self, index, shape, grid):
+        self.index = index
+        self.shape = tuple(int(v) for v in shape)  # (B, N, D, fH, fW)
+        self.grid = grid  # host (offset, dx, nx)
+
+    def check(self, shape, grid=None):
+        """Shape of the features against the index; with a host ``grid``
+        triple, its size against the index's (no device read)."""
+        if tuple(int(v) for v in shape) != self.shape:
+            raise ValueError(f'features {tuple(shape)} do not match the camera index {self.shape}')
+        if grid is not None and list(grid[2]) != list(self.grid[2]):
+            raise ValueError('the grid differs from the one the camera index was built on')
+
+
+def lss_index_cameras(frustum, camera2lidar_rots, camera2lidar_trans, intrins, post_rots,
+                      post_trans, dx, bx, nx, *, extra_rots=None, extra_trans=None, grid=None):
+    """``get_geometry`` (``base.py:82-126``) fused into the quantisation: the
+    frustum points are moved to the lidar frame and quantised inside one
+    kernel, never stored.  fp32 with each operation rounded once (combine =
+    rots inv(intrins) formed in double, rounded once); torch's matmul may
+    round differently, so a point within rounding distance of a voxel face
+    can fall in the neighbouring cell (the only difference from pooling
+    ``get_geometry``'s tensor)."""
+    P.require_gpu(camera2lidar_rots, camera2lidar_trans, intrins, post_rots, post_trans)
+    dev = camera2lidar_trans.device
+    B, N, _ = camera2lidar_trans.shape
+    offset, d, n = grid if grid is not None else host_grid(dx, bx, nx)
+    frustum = frustum.to(dev, torch.float32).contiguous()
+    mats = (camera2lidar_rots, camera2lidar_trans, intrins, post_rots, post_trans, extra_rots,
+            extra_trans)
+    idx = P.index_from_cameras(frustum, mats, B, N, offset, d, n)
+    D, fH, fW = frustum.shape[:3]
+    return CameraIndex(idx, (B, N, D, fH, fW), (offset, d, n))
 
 
 class BevPoolTransform(nn.Module):
@@ -213,8 +296,10 @@ class BevPoolTransform(nn.Module):
     refreshed if the parameters are modified in place) so the forward never
     synchronises."""
 
-    def __init__(self, xbound, ybound, zbound):
+    def __init__(self, xbound, ybound, zbound, cache_index=False):
         super().__init__()
+        self.cache_index = cache_index
+        self._index_cache = None
         self.xbound, self.ybound, self.zbound = xbound, ybound, zbound
         dx, bx, nx = gen_dx_bx(xbound, ybound, zbound)
         self.dx = nn.Parameter(dx, requires_grad=False)
@@ -235,6 +320,29 @@ class BevPoolTransform(nn.Module):
 
     def bev_pool(self, geom_feats, x):
         return lss_bev_pool(geom_feats, x, self.dx, self.bx, self.nx, grid=self.grid())
+
+    def index_cameras(self, frustum, camera2lidar_rots, camera2lidar_trans, intrins, post_rots,
+                      post_trans, extra_rots=None, extra_trans=None):
+        """:func:`lss_index_cameras` on this grid.  With ``cache_index`` set,
+        the last index is returned again while every input is the same
+        tensor object at the same version (static cameras, e.g. inference
+        with fixed calibration); any new or modified input recomputes it."""
+        args = (frustum, camera2lidar_rots, camera2lidar_trans, intrins, post_rots, post_trans,
+                extra_rots, extra_trans)
+        if self.cache_index and self._index_cache is not None:
+            key, idx = self._index_cache
+            if len(key) == len(args) and all(
+                    (a is None and k is None) or (k is not None and a is not None and k[0]() is a
+                                                  and k[1] == a._version)
+                    for k, a in zip(key, args)):
+                return idx
+        idx = lss_index_cameras(frustum, camera2lidar_rots, camera2lidar_trans, intrins,
+                                post_rots, post_trans, self.dx, self.bx, self.nx,
+                                extra_rots=extra_rots, extra_trans=extra_trans, grid=self.grid())
+        if self.cache_index:
+            self._index_cache = (tuple(None if a is None else (weakref.ref(a), a._version)
+                                       for a in args), idx)
+        return idx
 
     def bev_pool_depth(self, geom_feats, depth, context):
         return lss_bev_pool_depth(geom_feats, depth, context, self.dx, self.bx, self.nx,

@@ -92,6 +92,35 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
                           void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * As bevpool_quantize_geom, with the geometry computed per point from the
+ * camera matrices instead of read from a geometry tensor.  Replaces
+ * models/vtransforms/base.py:82-126 (get_geometry) followed by :139-158.
+ * fp32 arithmetic with every operation rounded separately, 3x3 products
+ * summed left to right; combine = rots inv(intrins) (the reference's
+ * linalg.solve, base.py:107-110) is formed in double and rounded once.
+ * torch's batched matmul rounds its own way, so a point lying within
+ * rounding distance of a voxel face can land in the neighbouring cell.
+ *
+ *   frustum      fp32 (D, fH, fW, 3) contiguous (create_frustum, base.py:67-80)
+ *   rots, intrins, post_rots   fp32 [n_batch * n_cams_per_batch][3][3]
+ *   trans, post_trans          fp32 [n_batch * n_cams_per_batch][3]
+ *                (camera b*N + n; camera2lidar rotation / translation,
+ *                intrinsics, image-augmentation rotation / translation)
+ *   extra_rots   fp32 [n_batch][3][3] or NULL (identity)   base.py:114-118
+ *   extra_trans  fp32 [n_batch][3] or NULL (zero)          base.py:119-123
+ * all row-major and contiguous.  Point order and everything else as
+ * bevpool_quantize_geom (n_points = n_batch * n_cams_per_batch * D*fH*fW).
+ */
+int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_t fW,
+                             const float *rots, const float *trans, const float *intrins,
+                             const float *post_rots, const float *post_trans,
+                             const float *extra_rots, const float *extra_trans,
+                             int32_t n_cams_per_batch, int32_t n_batch, const float offset[3],
+                             const float dx[3], const int32_t nx[3], int32_t *rank,
+                             int32_t *meta, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
+/*
  * Op-level ranks from integer coords (columns x, y, z, b), fused with the
  * first sort pass histogram.
  *

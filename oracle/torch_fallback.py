@@ -15,6 +15,11 @@ Pinning (see ``tests/test_oracle.py``):
   sort_perm        brute-force sorted((rank, index)) on tiny inputs.
   intervals        brute-force run-length encoding on tiny inputs.
   backward         brute-force gather on tiny inputs + the C restatement.
+  get_geometry     brute-force per-point float64 formula (R K^-1 by explicit
+                   inverse) with augmentations, the closed-form projection
+                   back onto the image for identity augmentation, and a planted
+                   inverse-for-transpose mistake.
+  pool_ranks       equal, bit for bit, to lss_bev_pool on the ranks of lss_index.
   lss_feature      brute-force loops (one fp32 product per element) and the
                    rearrange's index map on tiny inputs.
   lss_bev_pool_depth  brute-force sequential fp32 loops of depth*context per
@@ -129,6 +134,44 @@ def lss_bev_pool(geom_feats, x, dx, bx, nx):
     xk = xf[q.kept]
     ck = q.coords[q.kept]
     out = bev_pool(xk, ck, B, int(nx[2]), int(nx[0]), int(nx[1]))
+    return torch.cat(out.unbind(dim=2), 1)
+
+
+def get_geometry(frustum, camera2lidar_rots, camera2lidar_trans, intrins, post_rots,
+                 post_trans, extra_rots=None, extra_trans=None, dtype=torch.float32):
+    """``base.py:82-126`` in ``dtype``: undo the image augmentation
+    (subtract post_trans, multiply by post_rots^T -- the transpose, as the
+    reference writes it), scale (u, v) by depth, map by
+    combine = linalg.solve(K^T, R^T)^T = R K^-1, add the translation, then the
+    optional lidar augmentation.  (B, N, D, fH, fW, 3)."""
+    f = lambda t: t.to(dtype)
+    B, N, _ = camera2lidar_trans.shape
+    points = f(frustum) - f(post_trans).view(B, N, 1, 1, 1, 3)
+    points = f(post_rots).transpose(-1, -2).reshape(B, N, 1, 1, 1, 3, 3).matmul(
+        points.unsqueeze(-1))
+    points = torch.cat((points[..., :2, :] * points[..., 2:3, :], points[..., 2:3, :]), 5)
+    combine = torch.linalg.solve(f(intrins).transpose(-1, -2),
+                                 f(camera2lidar_rots).transpose(-1, -2)).transpose(-1, -2)
+    points = combine.reshape(B, N, 1, 1, 1, 3, 3).matmul(points).squeeze(-1)
+    points = points + f(camera2lidar_trans).view(B, N, 1, 1, 1, 3)
+    if extra_rots is not None:
+        points = f(extra_rots).view(B, 1, 1, 1, 1, 3, 3).matmul(points.unsqueeze(-1)).squeeze(-1)
+    if extra_trans is not None:
+        points = points + f(extra_trans).view(B, 1, 1, 1, 1, 3)
+    return points
+
+
+def pool_ranks(x2, rank, B, nx):
+    """``base.py:157-165`` from the ranks on: keep rank >= 0 (order-preserving
+    boolean gather), ``index_add_`` in point order into the
+    (B, Dz, X, Y) grid (rank = ((b*Dz + z)*X + x)*Y + y), then the
+    (B, C*Dz, X, Y) collapse.  x2 (N_all, C)."""
+    X, Y, Z = (int(v) for v in nx)
+    keep = rank >= 0
+    C = x2.shape[1]
+    out = x2.new_zeros((B * Z * X * Y, C))
+    out.index_add_(0, rank[keep], x2[keep])
+    out = out.view(B, Z, X, Y, C).permute(0, 4, 1, 2, 3)
     return torch.cat(out.unbind(dim=2), 1)
 
 
