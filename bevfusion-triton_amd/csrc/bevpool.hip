@@ -2664,16 +2664,16 @@ int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t gra
     return fail(BEVPOOL_EINVAL, "null argument");
   if (!scratch || scratch_bytes < bevpool_backward_scratch_bytes(n_cells, C, BEVPOOL_F32))
     return fail(BEVPOOL_ESPACE, "backward scratch too small");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  int st;
-  if ((st = launch_bev_to_rows(grad, 4, grad_stride_b, grad_stride_c, grad_stride_z, C,
-                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
-    return st;
   const int64_t n_pix = n_points / D;
   const size_t smem = size_t(2 * int64_t(D) + C) * kDgPix * sizeof(float);
   if (smem > 65536)
     return fail(BEVPOOL_EINVAL, "depth bins and channels too many (2*D + C = %lld > 1024)",
                 (long long)(2 * int64_t(D) + C));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int st;
+  if ((st = launch_bev_to_rows(grad, 4, grad_stride_b, grad_stride_c, grad_stride_z, C,
+                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
+    return st;
   const unsigned grid = xcd_grid(ceil_div(n_pix, kDgPix));
   LaunchTimer t("depth_grad", s);
   const float *g = static_cast<const float *>(scratch);

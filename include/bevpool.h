@@ -307,13 +307,14 @@ int bevpool_forward_depth(const float *depth, const float *context_rows, int32_t
  *                             (0 for a dropped point)
  *   grad_context[bn, c, hw] = sum_d g[cell(p_d), c] * depth[p_d]
  *                             over the pixel's D points p_d (kept ones)
- * Sums are fp32 in a fixed order (a butterfly over channels; d in order), so
- * results are deterministic and agree with the reference within fp32
- * rounding (the reference sums in torch's reduction order).
+ * Sums are fp32 in a fixed order (over channels: 16-lane partial sums then a
+ * fixed reduction tree; over depth bins: four interleaved sequential chains
+ * added in order), so results are deterministic and agree with the reference
+ * within fp32 rounding (the reference sums in torch's reduction order).
  *
  *   grad          fp32 BEV gradient; element (b, c, z, xy) at
  *                 b*grad_stride_b + c*grad_stride_c + z*grad_stride_z + xy
- *   C             <= 256
+ *   C             <= 256, and 2*D + C <= 1024
  *   grad_depth    out: fp32 [n_points]
  *   grad_context  out: fp32, element (bn, c, hw) at
  *                 bn*gctx_stride_bn + c*gctx_stride_c + hw

@@ -4,6 +4,7 @@ status codes (these calls fail before any HIP call, so no GPU is needed), and
 the Python surface mirrors the reference's checks and exception types."""
 from __future__ import annotations
 
+import ctypes
 import json
 import re
 
@@ -147,3 +148,47 @@ def test_synthetic_rig_shapes(pkg):
     assert geom[..., 0].numel() == 1_993_728
     # cameras 1.5 m high: the nearest depth bin lies within a few metres
     assert torch.isfinite(geom).all()
+
+
+def test_status_codes_new_entry_points_without_gpu(pkg):
+    """Argument checks of the depth-weighted, planar and camera entry points
+    return before any HIP call."""
+    lib = pkg.library()
+    meta = np.zeros(8, np.int32)
+    rank = np.zeros(64, np.int32)
+    ws = np.zeros(1 << 16, np.uint8)
+    buf = np.zeros(256, np.float32)
+    p = buf.ctypes.data
+    # forward_depth: C must be a positive multiple of 4
+    st = lib.bevpool_forward_depth(p, p, 6, 0, 1, 1, None, p, p, meta.ctypes.data, 1, 1, 1, 1,
+                                   1, 1, p, p, 1 << 20, None)
+    assert st == -1 and b'multiple of 4' in lib.bevpool_last_error()
+    # forward_depth: n_points must be a multiple of D*HW
+    st = lib.bevpool_forward_depth(p, p, 8, 7, 2, 2, None, p, p, meta.ctypes.data, 1, 1, 1, 1,
+                                   1, 1, p, p, 1 << 20, None)
+    assert st == -1 and b'multiple of D*HW' in lib.bevpool_last_error()
+    # backward_depth: C <= 256, and 2*D + C <= 1024
+    st = lib.bevpool_backward_depth(p, 1, 1, 1, 300, None, 4, 1, 4, p, p, p, p, 1, 1, 1, p, p,
+                                    1, 1, p, 1 << 30, None)
+    assert st == -1 and b'[1, 256]' in lib.bevpool_last_error()
+    st = lib.bevpool_backward_depth(p, 1, 1, 1, 80, rank.ctypes.data, 500, 500, 1, p, p, p, p, 1,
+                                    1, 1, p, p, 1, 1, p, 1 << 30, None)
+    assert st == -1 and b'2*D + C' in lib.bevpool_last_error()
+    # planar_rows / backward_planar
+    st = lib.bevpool_planar_rows(p, 1, 1, 1, 0, 4, p, None)
+    assert st == -1 and b'planar shape' in lib.bevpool_last_error()
+    assert lib.bevpool_planar_rows(p, 1, 1, 0, 4, 4, p, None) == 0  # empty: nothing to do
+    st = lib.bevpool_backward_planar(p, 1, 1, 1, 4, rank.ctypes.data, 10, p, p, 1, 1, 1, 4, p,
+                                     1, 1, p, 1 << 20, None)
+    assert st == -1 and b'multiple of S' in lib.bevpool_last_error()
+    # quantize_cameras: sizes and required matrices
+    f3 = lambda *v: (ctypes.c_float * 3)(*v)
+    i3 = lambda *v: (ctypes.c_int32 * 3)(*v)
+    st = lib.bevpool_quantize_cameras(p, 0, 1, 1, p, p, p, p, p, None, None, 1, 1,
+                                      f3(0, 0, 0), f3(1, 1, 1), i3(4, 4, 1), rank.ctypes.data,
+                                      meta.ctypes.data, ws.ctypes.data, ws.size, None)
+    assert st == -1 and b'frustum/camera sizes' in lib.bevpool_last_error()
+    st = lib.bevpool_quantize_cameras(p, 2, 2, 2, None, p, p, p, p, None, None, 1, 1,
+                                      f3(0, 0, 0), f3(1, 1, 1), i3(4, 4, 1), rank.ctypes.data,
+                                      meta.ctypes.data, ws.ctypes.data, ws.size, None)
+    assert st == -1 and b'camera matrices' in lib.bevpool_last_error()
