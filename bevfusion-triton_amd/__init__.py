@@ -11,6 +11,7 @@ ziyangyeh/bevfusion-triton behind the reference's own Python surface:
                                             depth (x) context product
   lss_index_cameras / CameraIndex           base.py:82-126 get_geometry fused into the
                                             quantisation (cacheable for static cameras)
+  legacy.bev_pool / legacy.QuickCumsumCuda  ops/bev_pool/bev_pool_legacy.py:53-108
 
 The kernels live in ``csrc/bevpool.hip`` and are reached through the C ABI of
 ``include/bevpool.h`` (``libbevpool_amd.so``, loaded by ``_lib``).  There is no
@@ -19,6 +20,7 @@ CPU or Triton fallback.
 The directory name is not a Python identifier; load it with
 ``__graft_entry__.load_package()`` (registers it as ``bevfusion_triton_amd``).
 """
+from . import legacy
 from ._lib import BevPoolError, LibraryNotBuilt, library
 from .bev_pool import BevPoolFunction, BevPoolIndexExport, bev_pool
 from .vtransform import (BevPoolTransform, CameraIndex, LSSIndexExport, create_frustum, gen_dx_bx, host_grid, lss_bev_pool, lss_bev_pool_depth,
@@ -36,6 +38,7 @@ __all__ = [
     'create_frustum',
     'gen_dx_bx',
     'host_grid',
+    'legacy',
     'library',
     'lss_bev_pool',
     'lss_bev_pool_depth',
