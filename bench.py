@@ -571,8 +571,10 @@ def camera_index(pkg, spec, module, x, dev):
 def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
     """The reference's CPU fallback, restated in torch (oracle/torch_fallback):
     quantise -> kept mask -> compaction -> index_add_ -> permute -> Z-collapse,
-    backward by autograd; same inputs as the GPU run.  Median of 5 after one
-    warm-up at the box's thread share, plus one single-thread run."""
+    backward by autograd; same inputs as the GPU run.  At the box's thread
+    share: one warm-up, then full steps until 10 s of CPU time have passed
+    (at least 5, at most 60), median; then the median of 3 single-thread
+    steps."""
     sys.path.insert(0, str(ROOT))
     from oracle import torch_fallback as ref
 
@@ -592,12 +594,16 @@ def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
     torch.set_num_threads(threads)
     log(f'[bench] cpu baseline, {threads} threads')
     one()
-    runs = [one() for _ in range(5)]
+    runs, t_start = [], time.perf_counter()
+    while len(runs) < 5 or (time.perf_counter() - t_start < 10.0 and len(runs) < 60):
+        runs.append(one())
     fwd = statistics.median(r[0] for r in runs)
     bwd = statistics.median(r[1] for r in runs)
     torch.set_num_threads(1)
     log('[bench] cpu baseline, 1 thread')
-    f1, b1 = one()
+    singles = [one() for _ in range(3)]
+    f1 = statistics.median(r[0] for r in singles)
+    b1 = statistics.median(r[1] for r in singles)
     torch.set_num_threads(prev)
     model = ''
     try:
@@ -613,7 +619,8 @@ def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
         'cores': threads,
         'kind': 'port',
         'sample': f'full det workload ({n_all} points, C=80): torch-CPU restatement of the '
-                  f'reference fallback, fwd+bwd, median of 5 after 1 warm-up',
+                  f'reference fallback, fwd+bwd, median of {len(runs)} steps (10 s of CPU work) '
+                  f'after 1 warm-up; single thread: median of 3',
         'fwd_ms': round(fwd * 1e3, 2),
         'bwd_ms': round(bwd * 1e3, 2),
         'single_thread': {'value': round(n_all / (f1 + b1), 1), 'fwd_ms': round(f1 * 1e3, 1),
