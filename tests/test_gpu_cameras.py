@@ -116,3 +116,51 @@ def test_camera_index_cache(pkg, cuda, synthetic):
     assert torch.equal(c.index.rank, b.index.rank)
     plain = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(cuda)
     assert plain.index_cameras(**inp) is not plain.index_cameras(**inp)
+
+
+def _small_rig(B, N, D, fH, fW, seed):
+    """Cameras of a tiny frustum (D*fH*fW points per camera), random poses
+    and augmentations, on a small grid."""
+    g = torch.Generator().manual_seed(seed)
+    ds = torch.linspace(2.0, 12.0, D)
+    us = torch.linspace(0, 63, fW)
+    vs = torch.linspace(0, 31, fH)
+    fr = torch.stack(torch.broadcast_tensors(us.view(1, 1, fW), vs.view(1, fH, 1),
+                                             ds.view(D, 1, 1)), -1).contiguous()
+    yaw = torch.rand(B, N, generator=g) * 6.283
+    c, s = torch.cos(yaw), torch.sin(yaw)
+    z, o = torch.zeros_like(c), torch.ones_like(c)
+    rots = torch.stack((torch.stack((s, z, c), -1), torch.stack((-c, z, s), -1),
+                        torch.stack((z, -o, z), -1)), -2)
+    trans = torch.rand(B, N, 3, generator=g) - 0.5
+    K = torch.tensor([[40.0, 0.0, 32.0], [0.0, 40.0, 16.0], [0.0, 0.0, 1.0]]).repeat(B, N, 1, 1)
+    pr = torch.eye(3).repeat(B, N, 1, 1) * (0.95 + 0.1 * torch.rand(B, N, 1, 1, generator=g))
+    pr[..., 2, 2] = 1.0
+    pt = torch.rand(B, N, 3, generator=g) * 4.0
+    pt[..., 2] = 0.0
+    return dict(frustum=fr, camera2lidar_rots=rots, camera2lidar_trans=trans, intrins=K,
+                post_rots=pr, post_trans=pt)
+
+
+@pytest.mark.parametrize('extra', ['none', 'rots', 'trans', 'both'])
+def test_camera_index_many_cameras_per_block(pkg, cuda, extra):
+    """8 points per camera: one 2048-point block spans up to 256 cameras, more
+    than the 16 it stages in LDS, so the per-point table path runs; extra_rots /
+    extra_trans given alone take identity / zero for the other."""
+    from bevfusion_triton_amd.synthetic import RigSpec
+
+    B, N = 4, 40
+    inp = _small_rig(B, N, 2, 2, 2, seed=21)
+    g = torch.Generator().manual_seed(22)
+    yaw = (torch.rand(B, generator=g) - 0.5) * 0.3
+    er = torch.zeros(B, 3, 3)
+    er[:, 0, 0], er[:, 0, 1], er[:, 1, 0], er[:, 1, 1] = (torch.cos(yaw), -torch.sin(yaw),
+                                                          torch.sin(yaw), torch.cos(yaw))
+    er[:, 2, 2] = 1.0
+    et = torch.rand(B, 3, generator=g) - 0.5
+    inp['extra_rots'] = er if extra in ('rots', 'both') else None
+    inp['extra_trans'] = et if extra in ('trans', 'both') else None
+    spec = RigSpec(xbound=(-14.0, 14.0, 0.7), ybound=(-14.0, 14.0, 0.7),
+                   zbound=(-10.0, 10.0, 20.0))
+    module = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(cuda)
+    check_ranks(pkg, cuda, spec, inp, module)
