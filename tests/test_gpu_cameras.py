@@ -164,3 +164,30 @@ def test_camera_index_many_cameras_per_block(pkg, cuda, extra):
                    zbound=(-10.0, 10.0, 20.0))
     module = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(cuda)
     check_ranks(pkg, cuda, spec, inp, module)
+
+
+def test_camera_index_on_side_stream(pkg, cuda, synthetic):
+    """The index built on a side stream while the main stream runs other work
+    (the depth net, in a model), handed over with an event: same bits as the
+    index built in line."""
+    spec = synthetic.CASES['det']
+    inp = to_dev(synthetic.camera_inputs(spec, seed=9, augment=True), cuda)
+    module = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(cuda)
+    module.grid()
+    x = synthetic.make_features(spec, device=cuda)
+    ref_out = module.bev_pool(module.index_cameras(**inp), x)
+    side = torch.cuda.Stream()
+    main = torch.cuda.current_stream()
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        ci = module.index_cameras(**inp)
+        ready = torch.cuda.Event()
+        ready.record(side)
+    busy = torch.randn(4096, 4096, device=cuda)
+    for _ in range(4):
+        busy = busy @ busy.t() * 1e-4  # stand-in for the producer on the main stream
+    main.wait_event(ready)
+    for t in (ci.index.rank, ci.index.keys, ci.index.cell_start, ci.index.cell_end, ci.index.meta):
+        t.record_stream(main)
+    out = module.bev_pool(ci, x)
+    assert_bit_equal(out, ref_out, 'index built on a side stream')
