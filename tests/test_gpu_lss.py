@@ -183,3 +183,25 @@ def test_lss_channel_first_odd_channels(pkg, cuda, synthetic):
     B, N, D, fH, fW = case.geom.shape[:5]
     cf = torch.randn(B, N, 6, D, fH, fW, generator=torch.Generator().manual_seed(4))
     check_planar(pkg, cuda, case, cf, lambda t: t.permute(0, 1, 3, 4, 5, 2))
+
+
+def test_lss_all_points_dropped(pkg, cuda, synthetic):
+    """Every point outside the grid: a zero map, zero gradients (the
+    reference's empty x[kept] pooled by index_add_ into zeros)."""
+    case = synthetic.make_case('tiny')
+    geom = case.geom.clone()
+    geom[..., 0] += 1000.0
+    module = pkg.BevPoolTransform(case.xbound, case.ybound, case.zbound).to(cuda)
+    x = case.x.to(cuda).requires_grad_(True)
+    out = module.bev_pool(geom.to(cuda), x)
+    dx, bx, nx = grid_of(case)
+    assert_bit_equal(out, ref.lss_bev_pool(geom, case.x, dx, bx, nx), 'all dropped forward')
+    out.sum().backward()
+    assert int(torch.count_nonzero(x.grad)) == 0
+    B, N, D, fH, fW = geom.shape[:5]
+    depth = torch.rand(B * N, D, fH, fW, device=cuda).requires_grad_(True)
+    context = torch.rand(B * N, 16, fH, fW, device=cuda).requires_grad_(True)
+    out_d = module.bev_pool_depth(geom.to(cuda), depth, context)
+    assert int(torch.count_nonzero(out_d)) == 0
+    out_d.sum().backward()
+    assert int(torch.count_nonzero(depth.grad)) == 0 and int(torch.count_nonzero(context.grad)) == 0
