@@ -5,7 +5,9 @@
 //
 //   index stage
 //     quantize_geom_kernel / coord_ranks_kernel  point -> int32 rank (-1 dropped)
-//                                                + radix pass-0 block histogram
+//       / quantize_frustum_kernel                + radix pass-0 block histogram
+//                                                (frustum: geometry computed from
+//                                                the camera matrices in-kernel)
 //     radix_scan_kernel                          per-digit exclusive scan of the
 //                                                block histograms (+ zero cell ranges)
 //     radix_scatter_kernel<from_rank>            stable wave-ballot ranked scatter;
@@ -15,9 +17,12 @@
 //     count_starts_kernel + scan_counts_kernel
 //       + interval_write_kernel                  compacted interval starts/lengths
 //   forward
-//     accum_rows_kernel<T>      ranges of sorted points (snapped to cell
-//                               boundaries), rows staged through LDS, one
-//                               sequential fp32 accumulator per channel
+//     accum_pipe_kernel<T,..>   ranges of 256 sorted points (snapped to cell
+//                               boundaries); loader waves gather 16-byte row
+//                               pieces through a register ring into LDS, one
+//                               summing wave keeps a sequential fp32
+//                               accumulator per channel
+//     accum_rows_kernel<T>      the same for rows that are not 16-byte pieces
 //     rows_to_bev_kernel<T>     cell-major rows -> channel-first tile via LDS
 //                               transpose; empty cells written as zero
 //   backward
