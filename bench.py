@@ -40,6 +40,9 @@ WORKLOAD = {
     'train': 'train_fp32_b4: configs[2] -- det shape, B=4, rig perturbations',
     'hires': 'hires_fp32_b2: configs[4] -- 64x176 fmap, 720x720 BEV, 10% OOB',
 }
+# every configuration of the reference's benchmark table, in table order
+# (bf16 is op level: the vtransform forces fp32, models/helper/amp.py:35-67)
+CONFIG_TABLE = ('det', 'seg', 'train', 'bf16', 'hires')
 
 
 def log(msg):
@@ -160,9 +163,11 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--profile-steps', type=int, default=10,
                     help='steps run with per-kernel HIP-event timing')
-    ap.add_argument('--mode', default='bench', choices=['bench', 'kernels'],
+    ap.add_argument('--mode', default='bench', choices=['bench', 'kernels', 'configs'],
                     help="'kernels': run --steps plain fwd+bwd steps and a 512 MiB device copy "
-                         '(the traffic calibrator for rocprofv3 --pmc passes), print nothing')
+                         "(the traffic calibrator for rocprofv3 --pmc passes), print nothing; "
+                         "'configs': fwd/bwd time of every benchmark configuration, one JSON "
+                         'line each')
     ap.add_argument('--fold-pmc', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='fold the counter_collection.csv files of a FETCH_SIZE and a WRITE_SIZE '
                          'pass of --mode kernels into profiles/traffic_<config>.json (no GPU)')
@@ -180,6 +185,10 @@ def main():
 
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
+    if args.mode == 'configs':
+        for name in CONFIG_TABLE:
+            print(json.dumps(config_figure(pkg, _lib, name, dev)), flush=True)
+        return
     log(f'[bench] building inputs for {args.config}')
     spec, geom_cpu, x_dev = make_inputs(pkg, args.config, dev)
     geom = geom_cpu.to(dev)
@@ -383,6 +392,101 @@ def main():
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline(spec, geom_cpu, x.detach().cpu(), g.cpu(), n_all)
     print(json.dumps(result), flush=True)
+
+
+def config_figure(pkg, lib, name, dev):
+    """fwd / bwd of one benchmark configuration: median of 20 back-to-back
+    steps by HIP events after 3 warm-ups, the accumulation kernel's average
+    by the library's launch events, and the path's algorithmic bandwidth.
+    fp32 configurations run the vtransform-level call on the full frustum;
+    bf16 runs the op-level bev_pool on the kept points (fp32 accumulation,
+    bf16 output and gradient)."""
+    log(f'[bench] config {name}')
+    spec, geom_cpu, x = make_inputs(pkg, name, dev)
+    geom = geom_cpu.to(dev)
+    module = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(dev)
+    C = spec.channels
+    n_all = geom[..., 0].numel()
+    exp = pkg.LSSIndexExport(geom, module.dx, module.bx, module.nx)
+    n_kept, n_occ = int(exp.perm.numel()), int(exp.starts.numel())
+    del exp
+    X, Y, Z = (int(v) for v in module.nx)
+    B = spec.batch
+    cells = B * X * Y * Z
+    s = x.element_size()
+    if spec.dtype == torch.float32:
+        x = x.detach().requires_grad_(True)
+        g = torch.randn((B, C * Z, X, Y), generator=torch.Generator(device=dev).manual_seed(0),
+                        device=dev)
+
+        def fwd():
+            return module.bev_pool(geom, x)
+
+        def bwd(out):
+            torch.autograd.grad(out, x, g)
+
+        fwd_b, bwd_b = alg_bytes(n_all, n_kept, n_occ, cells, C, s)
+        level, n_step = 'vtransform', n_all
+    else:
+        off, d, nx = module.grid()
+        q = ((geom.reshape(B, -1, 3) - torch.tensor(off, device=dev)) /
+             torch.tensor(d, device=dev))
+        kept = ((q > -1) & (q < torch.tensor(nx, device=dev, dtype=torch.float32))).all(-1)
+        b = torch.arange(B, device=dev).view(B, 1).expand(kept.shape)
+        coords = torch.cat((q.long(), b.unsqueeze(-1)), -1)[kept].to(torch.int32).contiguous()
+        feats = x.reshape(B, -1, C)[kept].contiguous().requires_grad_(True)
+        del x, q, kept, b
+        g = torch.randn((B, C, Z, X, Y), generator=torch.Generator(device=dev).manual_seed(0),
+                        device=dev).to(spec.dtype)
+
+        def fwd():
+            return pkg.bev_pool(feats, coords, B, Z, X, Y, check_bounds=False)
+
+        def bwd(out):
+            torch.autograd.grad(out, feats, g)
+
+        # op level: kept rows read, dense grid written; grid rows of occupied
+        # cells read, kept-row gradient written (no geometry, no zero rows)
+        fwd_b = s * C * n_kept + s * C * cells
+        bwd_b = s * C * n_occ + s * C * n_kept
+        level, n_step = 'op', n_kept
+    for _ in range(3):
+        bwd(fwd())
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(20):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        out = fwd()
+        e[1].record()
+        bwd(out)
+        e[2].record()
+        evs.append(e)
+    torch.cuda.synchronize()
+    t_fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+    t_bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+    lib.timing_reset()
+    lib.timing_enable(True)
+    for _ in range(5):
+        bwd(fwd())
+    torch.cuda.synchronize()
+    lib.timing_enable(False)
+    # per step (a kernel may launch more than once per step: two radix passes)
+    kt = {k: ms * 1e3 / 5 for k, (ms, n) in lib.timing_read().items()}
+    acc_us = kt.get('accum_rows')
+    acc_b = kernel_alg_bytes('accum_rows', n_all, n_kept, n_occ, cells, C, s)
+    t = (t_fwd + t_bwd) * 1e-3
+    return {
+        'config': name, 'level': level, 'dtype': str(spec.dtype).replace('torch.', ''),
+        'batch': B, 'bev': [X, Y, Z], 'frustum_points': n_all, 'n_kept': n_kept,
+        'n_occ': n_occ, 'fwd_us': round(t_fwd * 1e3, 1), 'bwd_us': round(t_bwd * 1e3, 1),
+        'points_per_s': round(n_step / t, 1),
+        'path_alg_MB': round((fwd_b + bwd_b) / 1e6, 1),
+        'path_achieved_GBps': round((fwd_b + bwd_b) / t / 1e9, 1),
+        'accum_rows_us': round(acc_us, 1) if acc_us else None,
+        'accum_rows_GBps': round(acc_b / (acc_us * 1e-6) / 1e9, 1) if acc_us else None,
+        'kernels_us_per_step': {k: round(v, 1) for k, v in sorted(kt.items())},
+    }
 
 
 def op_level(pkg, geom, x, module, dev):

@@ -117,6 +117,12 @@ inline unsigned xcd_grid(int64_t blocks) {
 #endif
 }
 
+// Grid of a kernel that walks the kSortTile tiles of the sort (at least one
+// block: block 0 also resets meta).  Such kernels take tile
+// xcd_chunk(blockIdx.x, gridDim.x), so the 32 tiles that share a 128-byte
+// line of a digit's histogram row are written from one XCD's L2.
+inline unsigned sort_grid(int64_t tiles) { return tiles > 0 ? xcd_grid(tiles) : 1u; }
+
 // ---------------------------------------------------------------------------
 // error reporting
 // ---------------------------------------------------------------------------
@@ -295,11 +301,12 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
   __shared__ int cnt[kMaxRadix];
   if (blockIdx.x == 0 && threadIdx.x < BEVPOOL_META_LEN)  // nothing else touches meta here
     meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
-  if (int(blockIdx.x) >= nblocks) return;  // the one block of an empty launch
+  const int tile = int(xcd_chunk(blockIdx.x, gridDim.x));
+  if (tile >= nblocks) return;  // grid padding, or the one block of an empty launch
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
-  const uint32_t base = uint32_t(blockIdx.x) * kSortTile;  // n_points < 2^31
+  const uint32_t base = uint32_t(tile) * kSortTile;  // n_points < 2^31
   const uint32_t n = uint32_t(n_points), uppb = uint32_t(ppb);
   // raw fp32 bits: lanes of a 16-byte load are never bit cast to float
   // while still in vector form (hipcc 7.2 folded such casts of lanes y/z/w
@@ -372,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + tile] = cnt[d];
 }
 
 // ---- geometry from camera matrices, fused with the quantisation -----------
@@ -469,12 +476,13 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
   __shared__ float lbat[kCamSlots][kBatchFloats];
   if (blockIdx.x == 0 && threadIdx.x < BEVPOOL_META_LEN)
     meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
-  if (int(blockIdx.x) >= nblocks) return;
+  const int tile = int(xcd_chunk(blockIdx.x, gridDim.x));
+  if (tile >= nblocks) return;
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
   const uint32_t n = uint32_t(n_points);
-  const uint32_t base = uint32_t(blockIdx.x) * kSortTile;
+  const uint32_t base = uint32_t(tile) * kSortTile;
   const uint32_t last = (base + kSortTile < n ? base + kSortTile : n) - 1;
   const uint32_t cam_lo = base / dhw, cam_hi = last / dhw;
   const bool staged = cam_hi - cam_lo < uint32_t(kCamSlots);
@@ -508,7 +516,7 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + tile] = cnt[d];
 }
 
 // ops/bev_pool/src/bev_pool_triton.py:34-39 in int64 (wrapping) arithmetic.
@@ -520,9 +528,11 @@ __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
   __shared__ int cnt[kMaxRadix];
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
+  const int tile = int(xcd_chunk(blockIdx.x, gridDim.x));
+  if (tile >= nblocks) return;  // grid padding
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
   __syncthreads();
-  const int64_t base = int64_t(blockIdx.x) * kSortTile;
+  const int64_t base = int64_t(tile) * kSortTile;
   const uint64_t cells = uint64_t(B * D * H * W);
   for (int k = 0; k < kItems; ++k) {
     const int64_t p = base + int64_t(k) * kThreads + threadIdx.x;
@@ -543,7 +553,7 @@ __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + tile] = cnt[d];
 }
 
 __global__ void init_meta_kernel(int32_t *meta) {
@@ -585,6 +595,24 @@ __global__ __launch_bounds__(kThreads) void radix_scan_kernel(
   }
 }
 
+// Counts the digits held by the 64 lanes of a wave into cnt with one LDS
+// atomic per run of equal digits in consecutive lanes (its first lane adds
+// the run length).  Sorted keys hold long runs of one digit, which a
+// per-lane atomic would serialise on one LDS address.  Lanes with valid ==
+// false count nothing and end any run.  All 64 lanes must be active.
+__device__ __forceinline__ void count_digit_runs(int *cnt, unsigned digit, bool valid) {
+  const unsigned d = valid ? digit : 0xffffffffu;
+  // digit of the lane below (wave shift right by one); lane 0 gets ~d
+  const unsigned below = unsigned(__builtin_amdgcn_update_dpp(int(~d), int(d), 0x138, 0xf, 0xf,
+                                                              false));
+  const bool head = d != below;
+  const uint64_t heads = __ballot(head);
+  const int lane = lane_id();
+  const uint64_t after = heads & ~((uint64_t(2) << lane) - 1);  // heads above this lane
+  const int next = after ? __builtin_ctzll(after) : 64;
+  if (valid && head) atomicAdd(&cnt[d], next - lane);
+}
+
 // Block histogram of one digit over the sorted keys of the previous pass.
 __global__ __launch_bounds__(kThreads) void radix_hist_kernel(
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
@@ -592,17 +620,25 @@ __global__ __launch_bounds__(kThreads) void radix_hist_kernel(
   __shared__ int cnt[kMaxRadix];
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
+  const int tile = int(xcd_chunk(blockIdx.x, gridDim.x));
+  if (tile >= nblocks) return;  // grid padding
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
   __syncthreads();
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
-  const int64_t base = int64_t(blockIdx.x) * kSortTile;
-#pragma unroll 4
+  const int64_t base = int64_t(tile) * kSortTile;
+  // all loads first (in bounds: past n they read key 0), then the counts
+  uint64_t key[kItems];
+#pragma unroll
   for (int k = 0; k < kItems; ++k) {
     const int64_t e = base + int64_t(k) * kThreads + threadIdx.x;
-    if (e < n) atomicAdd(&cnt[key_digit(keys[e], shift, mask)], 1);
+    key[k] = keys[e < n ? e : 0];
   }
+#pragma unroll
+  for (int k = 0; k < kItems; ++k)
+    count_digit_runs(cnt, key_digit(key[k], shift, mask),
+                     base + int64_t(k) * kThreads + threadIdx.x < n);
   __syncthreads();
-  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + blockIdx.x] = cnt[d];
+  for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + tile] = cnt[d];
 }
 
 // Stable scatter of one LSD radix pass.  Wave w of block b owns the 1024
@@ -676,8 +712,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
   // per-wave digit counts
   int *cnt = s_cnt + w * R;
 #pragma unroll
-  for (int k = 0; k < kItems; ++k)
-    if (valid[k]) atomicAdd(&cnt[key_digit(key[k], shift, mask)], 1);
+  for (int k = 0; k < kItems; ++k) count_digit_runs(cnt, key_digit(key[k], shift, mask), valid[k]);
   __syncthreads();
   for (int d = tid; d < R; d += kThreads) {
     int run = s_base[d];
@@ -2273,7 +2308,7 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
   {
     // also resets meta (block 0); an empty input still launches that block
     LaunchTimer t("quantize_geom", s);
-    const unsigned grid = L.sort_blocks > 0 ? unsigned(L.sort_blocks) : 1u;
+    const unsigned grid = sort_grid(L.sort_blocks);
     const bool vec = geom_row_stride == 3 && n_points >= 4 &&
                      reinterpret_cast<uintptr_t>(geom) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(rank) % 16 == 0;
@@ -2314,7 +2349,7 @@ int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_
   const CameraMats cm{rots, trans, intrins, post_rots, post_trans, extra_rots, extra_trans,
                       n_cams_per_batch};
   LaunchTimer t("quantize_cameras", s);
-  hipLaunchKernelGGL(quantize_frustum_kernel, dim3(unsigned(L.sort_blocks)), dim3(kThreads), 0, s,
+  hipLaunchKernelGGL(quantize_frustum_kernel, dim3(sort_grid(L.sort_blocks)), dim3(kThreads), 0, s,
                      frustum, n_points, uint32_t(dhw), cm, offset[0], offset[1], offset[2],
                      dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,
                      at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0], meta);
@@ -2346,12 +2381,12 @@ int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_point
   const DigitPlan plan = plan_digits(n_cells);
   LaunchTimer t("coord_ranks", s);
   if (coord_bytes == 4) {
-    hipLaunchKernelGGL(coord_ranks_kernel<int32_t>, dim3(unsigned(L.sort_blocks)), dim3(kThreads),
+    hipLaunchKernelGGL(coord_ranks_kernel<int32_t>, dim3(sort_grid(L.sort_blocks)), dim3(kThreads),
                        0, s, static_cast<const int32_t *>(coords), n_points, coords_row_stride,
                        int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
                        at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
   } else {
-    hipLaunchKernelGGL(coord_ranks_kernel<int64_t>, dim3(unsigned(L.sort_blocks)), dim3(kThreads),
+    hipLaunchKernelGGL(coord_ranks_kernel<int64_t>, dim3(sort_grid(L.sort_blocks)), dim3(kThreads),
                        0, s, static_cast<const int64_t *>(coords), n_points, coords_row_stride,
                        int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
                        at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
@@ -2386,7 +2421,7 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
     uint64_t *dst = ((plan.passes - 1 - pass) % 2 == 0) ? keys : tmp;
     if (pass > 0) {
       LaunchTimer t("radix_hist", s);
-      hipLaunchKernelGGL(radix_hist_kernel, dim3(nb), dim3(kThreads), 0, s, src, meta, hist, nb,
+      hipLaunchKernelGGL(radix_hist_kernel, dim3(sort_grid(nb)), dim3(kThreads), 0, s, src, meta, hist, nb,
                          plan.shift[pass], plan.bits[pass]);
       if ((st = check_launch("radix_hist"))) return st;
     }
