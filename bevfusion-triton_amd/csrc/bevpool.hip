@@ -268,14 +268,31 @@ struct BF16 {
 // index stage kernels
 // ---------------------------------------------------------------------------
 
+// n / d for n < 2^31 by multiply-high and shift (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", 1994): with
+// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (host side),
+// q = (mulhi(n, m) + n) >> s; mulhi(n, m) <= n keeps the sum in 32 bits.
+struct FastDiv {
+  uint32_t d, m, s;
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return (__umulhi(n, m) + n) >> s;
+  }
+};
+
+inline FastDiv make_fast_div(uint32_t d) {
+  uint32_t s = 0;
+  while ((uint64_t(1) << s) < d) ++s;
+  const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
+  return FastDiv{d, uint32_t(m), s};
+}
+
 // models/vtransforms/base.py:139-158: q = ((g - (bx - dx/2)) / dx).long(),
 // kept iff 0 <= q_k < nx[k].  In fp32, trunc(q) in [0, n) <=> q > -1 && q < n
 // (NaN fails both), which avoids converting out-of-range floats.
 // Rank: ops/bev_pool/src/bev_pool_triton.py:34-39 with (D, H, W) = (nz, nx, ny).
-__device__ __forceinline__ int quantize_point(float gx, float gy, float gz, uint32_t p,
-                                              uint32_t ppb, float o0, float o1, float o2,
-                                              float d0, float d1, float d2, int n0, int n1,
-                                              int n2) {
+__device__ __forceinline__ int quantize_point(float gx, float gy, float gz, int b, float o0,
+                                              float o1, float o2, float d0, float d1, float d2,
+                                              int n0, int n1, int n2) {
   const float q0 = (gx - o0) / d0;
   const float q1 = (gy - o1) / d1;
   const float q2 = (gz - o2) / d2;
@@ -283,7 +300,6 @@ __device__ __forceinline__ int quantize_point(float gx, float gy, float gz, uint
                     (q2 > -1.0f) & (q2 < float(n2));
   if (!kept) return -1;
   const int x = int(q0), y = int(q1), z = int(q2);
-  const int b = int(p / ppb);
   return ((b * n2 + z) * n0 + x) * n1 + y;
 }
 
@@ -293,7 +309,7 @@ __device__ __forceinline__ int quantize_point(float gx, float gy, float gz, uint
 // 16-byte rank store.  All groups' loads are issued before any is used.
 template <bool kVec>
 __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
-    const float *__restrict__ geom, int64_t n_points, int64_t gstride, int64_t ppb, float o0,
+    const float *__restrict__ geom, int64_t n_points, int64_t gstride, FastDiv ppb, float o0,
     float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
     int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits,
     int32_t *__restrict__ meta) {
@@ -307,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
   const unsigned mask = unsigned(R - 1);
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
   const uint32_t base = uint32_t(tile) * kSortTile;  // n_points < 2^31
-  const uint32_t n = uint32_t(n_points), uppb = uint32_t(ppb);
+  const uint32_t n = uint32_t(n_points);
   // raw fp32 bits: lanes of a 16-byte load are never bit cast to float
   // while still in vector form (hipcc 7.2 folded such casts of lanes y/z/w
   // into lane x)
@@ -361,8 +377,8 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
     for (int u = 0; u < 4; ++u) {
       r[u] = quantize_point(__builtin_bit_cast(float, g[k][3 * u]),
                             __builtin_bit_cast(float, g[k][3 * u + 1]),
-                            __builtin_bit_cast(float, g[k][3 * u + 2]), p0 + u, uppb, o0, o1, o2,
-                            d0, d1, d2, n0, n1, n2);
+                            __builtin_bit_cast(float, g[k][3 * u + 2]), int(ppb.div(p0 + u)),
+                            o0, o1, o2, d0, d1, d2, n0, n1, n2);
       if (r[u] >= 0 && p0 + u < n) atomicAdd(&cnt[unsigned(r[u]) & mask], 1);
     }
     if (kVec && p0 + 3 < n) {
@@ -467,7 +483,8 @@ __device__ __forceinline__ void frustum_point(const float *__restrict__ c,
 // more than kCamSlots cameras (frustums under ~140 points) builds each
 // point's table in registers instead.
 __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
-    const float *__restrict__ frustum, int64_t n_points, uint32_t dhw, CameraMats cm, float o0,
+    const float *__restrict__ frustum, int64_t n_points, FastDiv dhw, FastDiv npb, CameraMats cm,
+    float o0,
     float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
     int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits,
     int32_t *__restrict__ meta) {
@@ -484,21 +501,20 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
   const uint32_t n = uint32_t(n_points);
   const uint32_t base = uint32_t(tile) * kSortTile;
   const uint32_t last = (base + kSortTile < n ? base + kSortTile : n) - 1;
-  const uint32_t cam_lo = base / dhw, cam_hi = last / dhw;
+  const uint32_t cam_lo = dhw.div(base), cam_hi = dhw.div(last);
   const bool staged = cam_hi - cam_lo < uint32_t(kCamSlots);
   const bool extra = cm.has_extra();
-  const uint32_t ppb = dhw * uint32_t(cm.n_per_batch);  // points per batch
   if (staged && threadIdx.x <= cam_hi - cam_lo) {
     const uint32_t cam = cam_lo + threadIdx.x;
     camera_table(cm, cam, lcam[threadIdx.x]);
-    if (extra) batch_table(cm, cam / uint32_t(cm.n_per_batch), lbat[threadIdx.x]);
+    if (extra) batch_table(cm, npb.div(cam), lbat[threadIdx.x]);
   }
   __syncthreads();
   for (int k = 0; k < kItems; ++k) {
     const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
     int r = -1;
     if (p < n) {
-      const uint32_t cam = p / dhw, f = p - cam * dhw;
+      const uint32_t cam = dhw.div(p), f = p - cam * dhw.d;
       const float *fr = frustum + int64_t(f) * 3;
       float gx, gy, gz;
       if (staged) {
@@ -507,10 +523,10 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
       } else {
         float ct[kCamFloats], bt[kBatchFloats];
         camera_table(cm, cam, ct);
-        if (extra) batch_table(cm, cam / uint32_t(cm.n_per_batch), bt);
+        if (extra) batch_table(cm, npb.div(cam), bt);
         frustum_point(ct, extra ? bt : nullptr, fr[0], fr[1], fr[2], gx, gy, gz);
       }
-      r = quantize_point(gx, gy, gz, p, ppb, o0, o1, o2, d0, d1, d2, n0, n1, n2);
+      r = quantize_point(gx, gy, gz, int(npb.div(cam)), o0, o1, o2, d0, d1, d2, n0, n1, n2);
       if (r >= 0) atomicAdd(&cnt[unsigned(r) & mask], 1);
       rank[p] = r;
     }
@@ -984,24 +1000,6 @@ struct LoaderRing {
   int sq[kSlots];                // 16-byte column of slot i
 };
 
-// n / d for n < 2^31 by multiply-high and shift (Granlund & Montgomery,
-// "Division by invariant integers using multiplication", 1994): with
-// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (host side),
-// q = (mulhi(n, m) + n) >> s; mulhi(n, m) <= n keeps the sum in 32 bits.
-struct FastDiv {
-  uint32_t d, m, s;
-  __device__ __forceinline__ uint32_t div(uint32_t n) const {
-    return (__umulhi(n, m) + n) >> s;
-  }
-};
-
-inline FastDiv make_fast_div(uint32_t d) {
-  uint32_t s = 0;
-  while ((uint64_t(1) << s) < d) ++s;
-  const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
-  return FastDiv{d, uint32_t(m), s};
-}
-
 // Rows of the depth-weighted forward (fused depth x context pooling): the row
 // of point p = (bn*D + d)*HW + hw is context row pix = bn*HW + hw, weighted by
 // depth[p] (the reference materialises depth[p] * context[pix, c],
@@ -1369,6 +1367,12 @@ __device__ __forceinline__ bool load_tile_cells(int64_t cell0, int64_t n_cells,
 // block pays one memory latency before its stores.  Occupancy: cell_end != 0
 // (cell ranges are zeroed before the sort writes the occupied ones).
 constexpr int kTileSlots = kCellTile * (kTileChannels / 4) / kThreads;  // 8
+// bev_to_rows on grids of at least this many cells reads the occupancy of a
+// thread's 4 cells before its gradient loads (one more memory latency per
+// block, no loads for 4 empty cells); smaller grids issue every load up
+// front.  Measured on MI355X: 3-10% faster from 518,400 cells (B = 4 at
+// 360 x 360) up, slower at 129,600.  The same for rows_to_bev was slower.
+constexpr int64_t kOccFirstCells = 200000;
 
 template <typename T, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
@@ -1475,12 +1479,14 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
 // the occupied cells (raw bits copied).  With kVecBev each thread always
 // handles the same 4 cells (j = 4 * (tid % 16)) of channels tid / 16 + 16 it;
 // all its tile loads are issued up front (clamped in-bounds addresses,
-// empty cells included) together with the occupancy loads.
+// empty cells included) together with the occupancy loads, or, with
+// occ_first, after reading its 4 cells' occupancy (none when all 4 are
+// empty).
 template <typename TR, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
     const TR *__restrict__ grad, int C, int CT, const int32_t *__restrict__ cstart,
     const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
-    int64_t sc, int64_t sz, TR *__restrict__ rows) {
+    int64_t sc, int64_t sz, bool occ_first, TR *__restrict__ rows) {
   extern __shared__ u32x4 smem_b2r[];
   TR *tile = reinterpret_cast<TR *>(smem_b2r);  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
@@ -1497,6 +1503,14 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
     const bool live = cell0 + j < n_cells;  // then all 4 cells are (n_cells % 4 == 0)
     const int64_t offj =
         cell_offset(uint32_t(live ? cell0 + j : cell0), uint32_t(n_z), uint32_t(n_xy), sb, sz);
+    // sparse grids: the 4 cells' occupancy first, no gradient loads when all are empty
+    bool need = true;
+    if (occ_first) {
+      need = false;
+      if (live)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) need |= cend[cell0 + j + u] != 0;
+    }
     for (int c0 = 0; c0 < C; c0 += CT) {
       const int cb = C - c0 < CT ? C - c0 : CT;
       using V = typename std::conditional<sizeof(TR) == 4, u32x4, u32x2>::type;
@@ -1505,7 +1519,7 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
       for (int it = 0; it < kTileSlots; ++it) {
         int c = (tid >> 4) + 16 * it;
         c = c < cb ? c : 0;
-        v[it] = *reinterpret_cast<const V *>(grad + offj + int64_t(c0 + c) * sc);
+        v[it] = need ? *reinterpret_cast<const V *>(grad + offj + int64_t(c0 + c) * sc) : V{};
       }
       if (c0 == 0 && tid < kCellTile) occ[tid] = occ_mine;
 #pragma unroll
@@ -2249,11 +2263,12 @@ int launch_bev_to_rows(const void *grad, size_t es, int64_t gsb, int64_t gsc, in
   const bool vrow = (size_t(C) * es % 16 == 0) && (size_t(CT) * es % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(rows) % 16 == 0);
   const bool vbev = bev_vec_ok(grad, es, n_xy, gsb, gsc, gsz);
+  const bool occ_first = n_cells >= kOccFirstCells;
   LaunchTimer t("bev_to_rows", s);
 #define BEVPOOL_B2R(TR, VR, VB)                                                                \
   hipLaunchKernelGGL((bev_to_rows_kernel<TR, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,   \
                      static_cast<const TR *>(grad), C, CT, cell_start, cell_end, n_cells, n_z, \
-                     n_xy, gsb, gsc, gsz, static_cast<TR *>(rows))
+                     n_xy, gsb, gsc, gsz, occ_first, static_cast<TR *>(rows))
 #define BEVPOOL_B2R_T(TR)                                                                      \
   if (vrow && vbev) BEVPOOL_B2R(TR, true, true);                                              \
   else if (vrow) BEVPOOL_B2R(TR, true, false);                                                \
@@ -2309,12 +2324,16 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
     // also resets meta (block 0); an empty input still launches that block
     LaunchTimer t("quantize_geom", s);
     const unsigned grid = sort_grid(L.sort_blocks);
+    // batch index = point / points_per_batch (every point index is < 2^31)
+    const FastDiv ppb = make_fast_div(uint32_t(
+        points_per_batch < 1 ? 1 : (points_per_batch > (int64_t(1) << 31) ? (int64_t(1) << 31)
+                                                                          : points_per_batch)));
     const bool vec = geom_row_stride == 3 && n_points >= 4 &&
                      reinterpret_cast<uintptr_t>(geom) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(rank) % 16 == 0;
 #define BEVPOOL_QUANT(V)                                                                       \
   hipLaunchKernelGGL(quantize_geom_kernel<V>, dim3(grid), dim3(kThreads), 0, s, geom, n_points, \
-                     geom_row_stride, points_per_batch, offset[0], offset[1], offset[2], dx[0],  \
+                     geom_row_stride, ppb, offset[0], offset[1], offset[2], dx[0],               \
                      dx[1], dx[2], nx[0], nx[1], nx[2], rank, at<int32_t>(workspace, L.hist),   \
                      int(L.sort_blocks), plan.bits[0], meta)
     if (vec) BEVPOOL_QUANT(true); else BEVPOOL_QUANT(false);
@@ -2350,7 +2369,8 @@ int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_
                       n_cams_per_batch};
   LaunchTimer t("quantize_cameras", s);
   hipLaunchKernelGGL(quantize_frustum_kernel, dim3(sort_grid(L.sort_blocks)), dim3(kThreads), 0, s,
-                     frustum, n_points, uint32_t(dhw), cm, offset[0], offset[1], offset[2],
+                     frustum, n_points, make_fast_div(uint32_t(dhw)),
+                     make_fast_div(uint32_t(n_cams_per_batch)), cm, offset[0], offset[1], offset[2],
                      dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,
                      at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0], meta);
   return check_launch("quantize_cameras");
