@@ -14,6 +14,12 @@
 //                                                pass 0 also compacts kept points
 //     radix_hist_kernel                          block histograms of passes >= 1
 //     cell_ranges_kernel                         dense [start, end) per cell
+//     bucket_sort_kernel                         ranks of 11..20 bits: after one
+//                                                global pass by the high digit,
+//                                                one block per group sorts the low
+//                                                digit and writes its cell ranges
+//                                                (replaces the passes >= 1 and
+//                                                cell_ranges_kernel)
 //     count_starts_kernel + scan_counts_kernel
 //       + interval_write_kernel                  compacted interval starts/lengths
 //   forward
@@ -208,8 +214,27 @@ __device__ __forceinline__ unsigned key_digit(uint64_t k, int shift, unsigned ma
   return unsigned(k >> (32 + shift)) & mask;
 }
 
-// Exclusive scan of one int per thread across a 256-thread block.
-// `scratch` holds kWaves ints.  Every thread must call it.
+// Counts the digits held by the 64 lanes of a wave into cnt with one LDS
+// atomic per run of equal digits in consecutive lanes (its first lane adds
+// the run length).  Sorted keys hold long runs of one digit, which a
+// per-lane atomic would serialise on one LDS address.  Lanes with valid ==
+// false count nothing and end any run.  All 64 lanes must be active.
+__device__ __forceinline__ void count_digit_runs(int *cnt, unsigned digit, bool valid) {
+  const unsigned d = valid ? digit : 0xffffffffu;
+  // digit of the lane below (wave shift right by one); lane 0 gets ~d
+  const unsigned below = unsigned(__builtin_amdgcn_update_dpp(int(~d), int(d), 0x138, 0xf, 0xf,
+                                                              false));
+  const bool head = d != below;
+  const uint64_t heads = __ballot(head);
+  const int lane = lane_id();
+  const uint64_t after = heads & ~((uint64_t(2) << lane) - 1);  // heads above this lane
+  const int next = after ? __builtin_ctzll(after) : 64;
+  if (valid && head) atomicAdd(&cnt[d], next - lane);
+}
+
+// Exclusive scan of one int per thread across a block of kW waves (256
+// threads by default).  `scratch` holds kW ints.  Every thread must call it.
+template <int kW = kWaves>
 __device__ int block_exclusive_scan(int v, int *scratch, int *total) {
   const int lane = lane_id(), w = threadIdx.x >> 6;
   int x = v;
@@ -222,7 +247,7 @@ __device__ int block_exclusive_scan(int v, int *scratch, int *total) {
   __syncthreads();
   int before = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) {
+  for (int i = 0; i < kW; ++i) {
     int s = scratch[i];
     before += (i < w) ? s : 0;
     tot += s;
@@ -311,7 +336,7 @@ template <bool kVec>
 __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
     const float *__restrict__ geom, int64_t n_points, int64_t gstride, FastDiv ppb, float o0,
     float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
-    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits,
+    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int shift, int bits,
     int32_t *__restrict__ meta) {
   constexpr int kGroups = kItems / 4;
   __shared__ int cnt[kMaxRadix];
@@ -379,7 +404,7 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
                             __builtin_bit_cast(float, g[k][3 * u + 1]),
                             __builtin_bit_cast(float, g[k][3 * u + 2]), int(ppb.div(p0 + u)),
                             o0, o1, o2, d0, d1, d2, n0, n1, n2);
-      if (r[u] >= 0 && p0 + u < n) atomicAdd(&cnt[unsigned(r[u]) & mask], 1);
+      count_digit_runs(cnt, (unsigned(r[u]) >> shift) & mask, r[u] >= 0 && p0 + u < n);
     }
     if (kVec && p0 + 3 < n) {
       u32x4 w;
@@ -486,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
     const float *__restrict__ frustum, int64_t n_points, FastDiv dhw, FastDiv npb, CameraMats cm,
     float o0,
     float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
-    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int bits,
+    int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int shift, int bits,
     int32_t *__restrict__ meta) {
   __shared__ int cnt[kMaxRadix];
   __shared__ float lcam[kCamSlots][kCamFloats];
@@ -527,7 +552,7 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
         frustum_point(ct, extra ? bt : nullptr, fr[0], fr[1], fr[2], gx, gy, gz);
       }
       r = quantize_point(gx, gy, gz, int(npb.div(cam)), o0, o1, o2, d0, d1, d2, n0, n1, n2);
-      if (r >= 0) atomicAdd(&cnt[unsigned(r) & mask], 1);
+      if (r >= 0) atomicAdd(&cnt[(unsigned(r) >> shift) & mask], 1);
       rank[p] = r;
     }
   }
@@ -540,7 +565,7 @@ template <typename TC>
 __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
     const TC *__restrict__ coords, int64_t n_points, int64_t cstride, int64_t B, int64_t D,
     int64_t H, int64_t W, int32_t *__restrict__ rank, int32_t *__restrict__ meta,
-    int32_t *__restrict__ hist, int nblocks, int bits) {
+    int32_t *__restrict__ hist, int nblocks, int shift, int bits) {
   __shared__ int cnt[kMaxRadix];
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
@@ -560,7 +585,7 @@ __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
       int r = -1;
       if (r64 < cells) {  // unsigned compare also rejects negative int64 ranks
         r = int(r64);
-        atomicAdd(&cnt[unsigned(r) & mask], 1);
+        atomicAdd(&cnt[(unsigned(r) >> shift) & mask], 1);
       } else {
         atomicAdd(&meta[BEVPOOL_META_N_BAD], 1);
         atomicMin(&meta[BEVPOOL_META_FIRST_BAD], int(p));
@@ -609,24 +634,6 @@ __global__ __launch_bounds__(kThreads) void radix_scan_kernel(
     cstart[c] = 0;
     cend[c] = 0;
   }
-}
-
-// Counts the digits held by the 64 lanes of a wave into cnt with one LDS
-// atomic per run of equal digits in consecutive lanes (its first lane adds
-// the run length).  Sorted keys hold long runs of one digit, which a
-// per-lane atomic would serialise on one LDS address.  Lanes with valid ==
-// false count nothing and end any run.  All 64 lanes must be active.
-__device__ __forceinline__ void count_digit_runs(int *cnt, unsigned digit, bool valid) {
-  const unsigned d = valid ? digit : 0xffffffffu;
-  // digit of the lane below (wave shift right by one); lane 0 gets ~d
-  const unsigned below = unsigned(__builtin_amdgcn_update_dpp(int(~d), int(d), 0x138, 0xf, 0xf,
-                                                              false));
-  const bool head = d != below;
-  const uint64_t heads = __ballot(head);
-  const int lane = lane_id();
-  const uint64_t after = heads & ~((uint64_t(2) << lane) - 1);  // heads above this lane
-  const int next = after ? __builtin_ctzll(after) : 64;
-  if (valid && head) atomicAdd(&cnt[d], next - lane);
 }
 
 // Block histogram of one digit over the sorted keys of the previous pass.
@@ -756,6 +763,144 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
       const int pos = cnt[dg] + below;
       keys_out[pos] = key[k];
       if (below == 0) cnt[dg] = pos + __popcll(peers);
+    }
+  }
+}
+
+// Second half of the sort when the ranks need 11..20 bits.  One global pass
+// (radix_scatter_kernel<true> by the high digit rank >> lbits) has grouped
+// the kept keys by high digit, each group in point order.  Block b sorts
+// group b stably by the low lbits bits, so the keys end sorted by rank with
+// ties in point order, as two LSD passes would leave them, and writes the
+// dense [start, end) of the group's 2^lbits cells (0, 0 when empty), which
+// replaces cell_ranges_kernel and the zeroing of the cell ranges.
+// Wave w of kBucketWaves owns the w-th slice of the group (a multiple of 64
+// keys) and walks it 64 keys at a time, in order, twice: the first walk
+// counts its digits, the second puts each key at
+//   (group start) + (smaller digits in the group) + (same digit in earlier
+//   waves) + (same digit earlier in this wave),
+// the last term from a ballot-built peer mask as in radix_scatter_kernel.
+// Keys are loaded kBucketBatch sub-batches at a time; a wave whose slice
+// fits in one batch keeps it in registers for the second walk.  Otherwise
+// the second walk drains each batch's loads before its first key store:
+// vmcnt counts loads and stores together, so a wait for a load issued after
+// a store would also wait for the store.  Dynamic LDS:
+// kBucketWaves * 2^lbits ints (16 waves up to 512 digits, 8 at 1024: at most
+// 64 KB per block).
+#ifndef BEVPOOL_BUCKET_BATCH
+#define BEVPOOL_BUCKET_BATCH 16
+#endif
+constexpr int kBucketBatch = BEVPOOL_BUCKET_BATCH;
+
+template <int kBucketWaves>
+__global__ __launch_bounds__(64 * kBucketWaves) void bucket_sort_kernel(
+    const uint64_t *__restrict__ keys_in, const int32_t *__restrict__ totals, int n_buckets,
+    int64_t n_cells, uint64_t *__restrict__ keys_out, int32_t *__restrict__ cstart,
+    int32_t *__restrict__ cend, int lbits) {
+  constexpr int kBucketThreads = 64 * kBucketWaves;
+  extern __shared__ int s_cnt[];  // [kBucketWaves][R]
+  __shared__ int s_scan[kBucketWaves];
+  // block i takes group i: the large groups (cells near the cameras) are
+  // consecutive, and round-robin blocks spread them over the XCDs
+  const int bkt = int(blockIdx.x);
+  if (bkt >= n_buckets) return;
+  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
+  const int R = 1 << lbits;
+  const unsigned mask = unsigned(R - 1);
+
+  // group start = keys of smaller high digits
+  int part = 0;
+  for (int d = tid; d < bkt; d += kBucketThreads) part += totals[d];
+  int gs;
+  block_exclusive_scan<kBucketWaves>(part, s_scan, &gs);
+  const int gn = totals[bkt];
+  for (int d = tid; d < kBucketWaves * R; d += kBucketThreads) s_cnt[d] = 0;
+  const int64_t q = (int64_t(gn) + kBucketThreads - 1) / kBucketThreads * 64;  // keys per wave
+  const int64_t ge = int64_t(gs) + gn;
+  const int wb = int(gs + w * q < ge ? gs + w * q : ge);
+  const int we = int(gs + (w + 1) * q < ge ? gs + (w + 1) * q : ge);
+  __syncthreads();
+
+  int *cnt = s_cnt + w * R;
+  uint64_t key[kBucketBatch];
+  const bool resident = we - wb <= 64 * kBucketBatch;  // wave-uniform
+  for (int e0 = wb; e0 < we; e0 += 64 * kBucketBatch) {
+    // sub-batches past the slice end are skipped (wave-uniform tests)
+#pragma unroll
+    for (int j = 0; j < kBucketBatch; ++j) {
+      const int e = e0 + 64 * j + lane;
+      if (e0 + 64 * j < we) key[j] = keys_in[e < we ? e : wb];
+    }
+#pragma unroll
+    for (int j = 0; j < kBucketBatch; ++j)
+      if (e0 + 64 * j < we)
+        count_digit_runs(cnt, key_digit(key[j], 0, mask), e0 + 64 * j + lane < we);
+  }
+  __syncthreads();
+
+  // digit starts within the group (digits kPer * tid + i), the cells'
+  // ranges, per-wave bases
+  constexpr int kPer = kMaxRadix / kBucketThreads;  // digits per thread (1 or 2)
+  int tot[kPer], tsum = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = kPer * tid + i;
+    tot[i] = 0;
+    if (d < R)
+#pragma unroll
+      for (int ww = 0; ww < kBucketWaves; ++ww) tot[i] += s_cnt[ww * R + d];
+    tsum += tot[i];
+  }
+  int gtotal;
+  int ex = gs + block_exclusive_scan<kBucketWaves>(tsum, s_scan, &gtotal);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = kPer * tid + i;
+    if (d < R) {
+      const int64_t cell = int64_t(bkt) * R + d;
+      if (cell < n_cells) {
+        cstart[cell] = tot[i] ? ex : 0;
+        cend[cell] = tot[i] ? ex + tot[i] : 0;
+      }
+      int run = ex;
+#pragma unroll
+      for (int ww = 0; ww < kBucketWaves; ++ww) {
+        const int c = s_cnt[ww * R + d];
+        s_cnt[ww * R + d] = run;
+        run += c;
+      }
+    }
+    ex += tot[i];
+  }
+  __syncthreads();
+
+  const uint64_t below_mask = lanes_below();
+  for (int e0 = wb; e0 < we; e0 += 64 * kBucketBatch) {
+    if (!resident) {
+#pragma unroll
+      for (int j = 0; j < kBucketBatch; ++j) {
+        const int e = e0 + 64 * j + lane;
+        if (e0 + 64 * j < we) key[j] = keys_in[e < we ? e : wb];
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the batch is in registers
+    }
+#pragma unroll
+    for (int j = 0; j < kBucketBatch; ++j) {
+      if (e0 + 64 * j >= we) break;
+      const bool valid = e0 + 64 * j + lane < we;
+      const unsigned dg = key_digit(key[j], 0, mask);
+      uint64_t peers = __ballot(valid);
+      for (int b = 0; b < lbits; ++b) {
+        const bool bit = (dg >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        peers &= bit ? bal : ~bal;
+      }
+      if (valid) {
+        const int below = __popcll(peers & below_mask);
+        const int pos = cnt[dg] + below;
+        keys_out[pos] = key[j];
+        if (below == 0) cnt[dg] = pos + __popcll(peers);
+      }
     }
   }
 }
@@ -2058,10 +2203,17 @@ __global__ __launch_bounds__(kThreads) void depth_grad_kernel(
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// LSD passes of at most kMaxDigitBits bits each; or, for ranks of 11..20
+// bits (local_bits > 0), one global pass by the high digit (shift[0] =
+// local_bits) and bucket_sort_kernel for the low local_bits bits.
+#ifndef BEVPOOL_BUCKET_SORT
+#define BEVPOOL_BUCKET_SORT 1
+#endif
 struct DigitPlan {
   int passes = 1;
   int bits[4] = {1, 0, 0, 0};
   int shift[4] = {0, 0, 0, 0};
+  int local_bits = 0;
 };
 
 DigitPlan plan_digits(int64_t n_cells) {
@@ -2069,6 +2221,12 @@ DigitPlan plan_digits(int64_t n_cells) {
   for (uint64_t v = uint64_t(n_cells > 1 ? n_cells - 1 : 0); v; v >>= 1) ++total_bits;
   if (total_bits < 1) total_bits = 1;
   DigitPlan p;
+  if (BEVPOOL_BUCKET_SORT && total_bits > kMaxDigitBits && total_bits <= 2 * kMaxDigitBits) {
+    p.bits[0] = (total_bits + 1) / 2;  // high digit: global pass
+    p.local_bits = total_bits - p.bits[0];
+    p.shift[0] = p.local_bits;
+    return p;
+  }
   p.passes = int((total_bits + kMaxDigitBits - 1) / kMaxDigitBits);
   const int per = (total_bits + p.passes - 1) / p.passes;
   int shift = 0;
@@ -2335,7 +2493,7 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
   hipLaunchKernelGGL(quantize_geom_kernel<V>, dim3(grid), dim3(kThreads), 0, s, geom, n_points, \
                      geom_row_stride, ppb, offset[0], offset[1], offset[2], dx[0],               \
                      dx[1], dx[2], nx[0], nx[1], nx[2], rank, at<int32_t>(workspace, L.hist),   \
-                     int(L.sort_blocks), plan.bits[0], meta)
+                     int(L.sort_blocks), plan.shift[0], plan.bits[0], meta)
     if (vec) BEVPOOL_QUANT(true); else BEVPOOL_QUANT(false);
 #undef BEVPOOL_QUANT
   }
@@ -2372,7 +2530,8 @@ int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_
                      frustum, n_points, make_fast_div(uint32_t(dhw)),
                      make_fast_div(uint32_t(n_cams_per_batch)), cm, offset[0], offset[1], offset[2],
                      dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,
-                     at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0], meta);
+                     at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0], plan.bits[0],
+                     meta);
   return check_launch("quantize_cameras");
 }
 
@@ -2404,12 +2563,14 @@ int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_point
     hipLaunchKernelGGL(coord_ranks_kernel<int32_t>, dim3(sort_grid(L.sort_blocks)), dim3(kThreads),
                        0, s, static_cast<const int32_t *>(coords), n_points, coords_row_stride,
                        int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
-                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
+                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0],
+                       plan.bits[0]);
   } else {
     hipLaunchKernelGGL(coord_ranks_kernel<int64_t>, dim3(sort_grid(L.sort_blocks)), dim3(kThreads),
                        0, s, static_cast<const int64_t *>(coords), n_points, coords_row_stride,
                        int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
-                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.bits[0]);
+                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0],
+                       plan.bits[0]);
   }
   return check_launch("coord_ranks");
 }
@@ -2437,8 +2598,9 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
   }
   const int nb = int(L.sort_blocks);
   const uint64_t *src = nullptr;
+  const bool bucketed = plan.local_bits > 0;
   for (int pass = 0; pass < plan.passes; ++pass) {
-    uint64_t *dst = ((plan.passes - 1 - pass) % 2 == 0) ? keys : tmp;
+    uint64_t *dst = bucketed ? tmp : (((plan.passes - 1 - pass) % 2 == 0) ? keys : tmp);
     if (pass > 0) {
       LaunchTimer t("radix_hist", s);
       hipLaunchKernelGGL(radix_hist_kernel, dim3(sort_grid(nb)), dim3(kThreads), 0, s, src, meta, hist, nb,
@@ -2448,7 +2610,8 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
     {
       LaunchTimer t("radix_scan", s);
       hipLaunchKernelGGL(radix_scan_kernel, dim3(1u << plan.bits[pass]), dim3(kThreads), 0, s,
-                         hist, nb, totals, cell_start, cell_end, pass == 0 ? n_cells : 0);
+                         hist, nb, totals, cell_start, cell_end,
+                         pass == 0 && !bucketed ? n_cells : 0);
       if ((st = check_launch("radix_scan"))) return st;
     }
     {
@@ -2465,6 +2628,21 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
       if ((st = check_launch("radix_scatter"))) return st;
     }
     src = dst;
+  }
+  if (bucketed) {
+    // groups of equal high digit -> sorted keys and the dense cell ranges
+    LaunchTimer t("bucket_sort", s);
+    const int64_t n_buckets = ceil_div(n_cells, int64_t(1) << plan.local_bits);
+    if (plan.local_bits <= 9) {
+      hipLaunchKernelGGL(bucket_sort_kernel<16>, dim3(unsigned(n_buckets)), dim3(16 * 64),
+                         size_t(16) << plan.local_bits << 2, s, src, totals, int(n_buckets),
+                         n_cells, keys, cell_start, cell_end, plan.local_bits);
+    } else {
+      hipLaunchKernelGGL(bucket_sort_kernel<8>, dim3(unsigned(n_buckets)), dim3(8 * 64),
+                         size_t(8) << plan.local_bits << 2, s, src, totals, int(n_buckets),
+                         n_cells, keys, cell_start, cell_end, plan.local_bits);
+    }
+    return check_launch("bucket_sort");
   }
   {
     LaunchTimer t("cell_ranges", s);

@@ -144,6 +144,48 @@ def test_shapes_and_edges(pkg, cuda, N, sizes, C):
     assert_bit_equal(grad, grad32, 'bwd')
 
 
+@pytest.mark.parametrize('name,sizes', [
+    ('11-bit ranks, 2-cell groups', (1, 1, 5, 205)),
+    ('20-bit ranks, 1024-cell groups', (1, 1, 1024, 1024)),
+    ('17-bit ranks, one group holding most points', (1, 1, 360, 360)),
+])
+def test_bucket_sort_edges(pkg, cuda, name, sizes):
+    """Ranks of 11..20 bits: one global pass by the high 10 bits, then one
+    block per group sorts the low bits and writes the group's cell ranges.
+    Cases: the smallest groups, the largest rank space, and one group far
+    larger than the rest (90% of the points in 3 cells, sizes not multiples
+    of 64), with empty groups around it."""
+    N = 120000
+    feats, coords = rand_case(N, 8, *sizes, seed=11)
+    if 'one group' in name:
+        g = torch.Generator().manual_seed(12)
+        hot = torch.rand(N, generator=g) < 0.9
+        cell = torch.randint(0, 3, (N,), generator=g)
+        coords[hot, 0] = 200  # x: cells 200*360 + 100..102 share one group
+        coords[hot, 1] = 100 + cell[hot].to(coords.dtype)
+    B, D, H, W = sizes
+    exp = pkg.BevPoolIndexExport(coords.to(cuda), *sizes)
+    ranks = ref.flatten_ranks(coords, *sizes)
+    perm = ref.sort_perm(ranks)
+    assert torch.equal(exp.perm.cpu(), perm), name
+    starts, lengths = ref.intervals(ranks[perm])
+    assert torch.equal(exp.starts.cpu(), starts), name
+    assert torch.equal(exp.lengths.cpu(), lengths), name
+    # dense cell ranges: [start, end) of every occupied cell, (0, 0) elsewhere
+    n_cells = B * D * H * W
+    cs = torch.zeros(n_cells, dtype=torch.int32)
+    ce = torch.zeros(n_cells, dtype=torch.int32)
+    cells = ranks[perm][starts.long()]
+    cs[cells] = starts
+    ce[cells] = starts + lengths
+    assert torch.equal(exp.index.cell_start.cpu(), cs), name
+    assert torch.equal(exp.index.cell_end.cpu(), ce), name
+    out, grad, up = run_op(pkg, feats, coords, sizes, cuda)
+    out32, grad32 = oracle_op(feats, coords, sizes, up)
+    assert_bit_equal(out, out32, f'{name} fwd')
+    assert_bit_equal(grad, grad32, f'{name} bwd')
+
+
 def test_large_rank_space(pkg, cuda):
     """2^21 cells: three radix passes."""
     sizes = (2, 1, 1024, 1024)
