@@ -80,6 +80,8 @@ def kernel_alg_bytes(name, n_all, n_kept, n_occ, cells, C, s=4):
         'bev_to_rows': 2 * s * C * n_occ + 8 * cells,
         # geometry (read) + ranks (written)
         'quantize_geom': 12 * n_all + 4 * n_all,
+        # grouped keys (read) + sorted keys (written) + dense cell ranges
+        'bucket_sort': 16 * n_kept + 8 * cells,
     }
     return table.get(name)
 
@@ -91,7 +93,8 @@ KERNEL_TIMER_NAMES = (
     ('bev_to_rows_kernel', 'bev_to_rows'), ('quantize_geom_kernel', 'quantize_geom'),
     ('coord_ranks_kernel', 'coord_ranks'), ('radix_scatter_kernel', 'radix_scatter'),
     ('radix_hist_kernel', 'radix_hist'), ('radix_scan_kernel', 'radix_scan'),
-    ('cell_ranges_kernel', 'cell_ranges'), ('init_meta', 'init_meta'),
+    ('cell_ranges_kernel', 'cell_ranges'), ('bucket_sort_kernel', 'bucket_sort'),
+    ('init_meta', 'init_meta'),
 )
 CALIBRATOR_BYTES = 512 << 20  # the --mode kernels device copy
 
