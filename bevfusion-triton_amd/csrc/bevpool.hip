@@ -232,6 +232,38 @@ __device__ __forceinline__ void count_digit_runs(int *cnt, unsigned digit, bool 
   if (valid && head) atomicAdd(&cnt[d], next - lane);
 }
 
+// OR of v over the 64 lanes (all active), in every lane's SGPR: DPP row
+// shifts, row broadcasts 15 / 31, lane 63.
+__device__ __forceinline__ unsigned wave_or(unsigned v) {
+  int x = int(v);
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return unsigned(__builtin_amdgcn_readlane(x, 63));
+}
+
+// The valid lanes of the wave whose digit equals this lane's (a stable
+// in-wave rank is the count of them below this lane).  Only the digit bits
+// that differ between valid lanes can split them: one wave OR finds those,
+// and each costs a ballot and a per-lane 64-bit combine (the VALU cost of
+// the rank).  Sorted and clustered keys leave most bits uniform in a wave.
+// All 64 lanes must be active.
+__device__ __forceinline__ uint64_t peer_mask(unsigned dg, bool valid) {
+  const uint64_t vm = __ballot(valid);
+  if (vm == 0) return 0;
+  const unsigned d0 = unsigned(__builtin_amdgcn_readlane(int(dg), int(__builtin_ctzll(vm))));
+  uint64_t peers = vm;
+  for (unsigned m = wave_or(valid ? dg ^ d0 : 0u); m; m &= m - 1) {
+    const bool bit = (dg >> __builtin_ctz(m)) & 1u;
+    const uint64_t bal = __ballot(bit);
+    peers &= bit ? bal : ~bal;
+  }
+  return peers;
+}
+
 // Exclusive scan of one int per thread across a block of kW waves (256
 // threads by default).  `scratch` holds kW ints.  Every thread must call it.
 template <int kW = kWaves>
@@ -752,12 +784,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 #pragma unroll
   for (int k = 0; k < kItems; ++k) {
     const unsigned dg = key_digit(key[k], shift, mask);
-    uint64_t peers = __ballot(valid[k]);
-    for (int b = 0; b < bits; ++b) {
-      const bool bit = (dg >> b) & 1u;
-      const uint64_t bal = __ballot(bit);
-      peers &= bit ? bal : ~bal;
-    }
+    const uint64_t peers = peer_mask(dg, valid[k]);
     if (valid[k]) {
       const int below = __popcll(peers & below_mask);
       const int pos = cnt[dg] + below;
@@ -889,12 +916,7 @@ __global__ __launch_bounds__(64 * kBucketWaves) void bucket_sort_kernel(
       if (e0 + 64 * j >= we) break;
       const bool valid = e0 + 64 * j + lane < we;
       const unsigned dg = key_digit(key[j], 0, mask);
-      uint64_t peers = __ballot(valid);
-      for (int b = 0; b < lbits; ++b) {
-        const bool bit = (dg >> b) & 1u;
-        const uint64_t bal = __ballot(bit);
-        peers &= bit ? bal : ~bal;
-      }
+      const uint64_t peers = peer_mask(dg, valid);
       if (valid) {
         const int below = __popcll(peers & below_mask);
         const int pos = cnt[dg] + below;
