@@ -807,24 +807,24 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 //   (group start) + (smaller digits in the group) + (same digit in earlier
 //   waves) + (same digit earlier in this wave),
 // the last term from a ballot-built peer mask as in radix_scatter_kernel.
-// Keys are loaded kBucketBatch sub-batches at a time; a wave whose slice
+// Keys are loaded kBucketBatch sub-batches (of 64) at a time; a wave whose slice
 // fits in one batch keeps it in registers for the second walk.  Otherwise
 // the second walk drains each batch's loads before its first key store:
 // vmcnt counts loads and stores together, so a wait for a load issued after
 // a store would also wait for the store.  Dynamic LDS:
 // kBucketWaves * 2^lbits ints (16 waves up to 512 digits, 8 at 1024: at most
 // 64 KB per block).
-#ifndef BEVPOOL_BUCKET_BATCH
-#define BEVPOOL_BUCKET_BATCH 16
-#endif
-constexpr int kBucketBatch = BEVPOOL_BUCKET_BATCH;
 
 template <int kBucketWaves>
-__global__ __launch_bounds__(64 * kBucketWaves) void bucket_sort_kernel(
+__global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
     const uint64_t *__restrict__ keys_in, const int32_t *__restrict__ totals, int n_buckets,
     int64_t n_cells, uint64_t *__restrict__ keys_out, int32_t *__restrict__ cstart,
     int32_t *__restrict__ cend, int lbits) {
   constexpr int kBucketThreads = 64 * kBucketWaves;
+  // sub-batches per load batch: 8 keeps the 16-wave kernel within 64 VGPRs
+  // (two blocks per CU); the 8-wave kernel (1024 digits, larger groups)
+  // gains from 16
+  constexpr int kBucketBatch = kBucketWaves >= 16 ? 8 : 16;
   extern __shared__ int s_cnt[];  // [kBucketWaves][R]
   __shared__ int s_scan[kBucketWaves];
   // block i takes group i: the large groups (cells near the cameras) are
