@@ -140,8 +140,13 @@ int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_point
                         void *stream);
 
 /*
- * Stream compaction of kept points + stable LSD radix sort of their ranks
- * + dense per-cell point ranges.
+ * Stream compaction of kept points + stable radix sort of their ranks
+ * + dense per-cell point ranges.  Ranks of 11..20 bits take one global pass
+ * by the high digit and one block per group of equal high digit for the
+ * low digit (that block also writes the group's cell ranges); other rank
+ * widths take LSD passes of at most 10 bits.  Both give the same keys.  The
+ * index stage's histograms must come from the quantise / coord-ranks call
+ * made with the same n_cells.
  *
  * Replaces the kept-point compaction of models/vtransforms/base.py:157-158
  * and the sort of ops/bev_pool/bev_pool_legacy.py:102-104, with the legacy
