@@ -567,25 +567,49 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
     if (extra) batch_table(cm, npb.div(cam), lbat[threadIdx.x]);
   }
   __syncthreads();
-  for (int k = 0; k < kItems; ++k) {
-    const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
-    int r = -1;
-    if (p < n) {
-      const uint32_t cam = dhw.div(p), f = p - cam * dhw.d;
-      const float *fr = frustum + int64_t(f) * 3;
+  if (staged) {
+    // all frustum loads first (points past n reload point n - 1), then the
+    // products; digit counts by runs (every lane active)
+    float fx[kItems], fy[kItems], fz[kItems];
+    uint32_t camv[kItems];
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
+      const uint32_t pc = p < n ? p : n - 1;
+      const uint32_t cam = dhw.div(pc), f = pc - cam * dhw.d;
+      camv[k] = cam;
+      fx[k] = frustum[int64_t(f) * 3];
+      fy[k] = frustum[int64_t(f) * 3 + 1];
+      fz[k] = frustum[int64_t(f) * 3 + 2];
+    }
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
+      const uint32_t c = camv[k] - cam_lo;
       float gx, gy, gz;
-      if (staged) {
-        frustum_point(lcam[cam - cam_lo], extra ? lbat[cam - cam_lo] : nullptr, fr[0], fr[1],
-                      fr[2], gx, gy, gz);
-      } else {
+      frustum_point(lcam[c], extra ? lbat[c] : nullptr, fx[k], fy[k], fz[k], gx, gy, gz);
+      const int r = quantize_point(gx, gy, gz, int(npb.div(camv[k])), o0, o1, o2, d0, d1, d2, n0,
+                                   n1, n2);
+      count_digit_runs(cnt, (unsigned(r) >> shift) & mask, p < n && r >= 0);
+      if (p < n) rank[p] = r;
+    }
+  } else {
+    // more cameras than LDS slots: each point's tables in registers
+    for (int k = 0; k < kItems; ++k) {
+      const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
+      int r = -1;
+      if (p < n) {
+        const uint32_t cam = dhw.div(p), f = p - cam * dhw.d;
+        const float *fr = frustum + int64_t(f) * 3;
+        float gx, gy, gz;
         float ct[kCamFloats], bt[kBatchFloats];
         camera_table(cm, cam, ct);
         if (extra) batch_table(cm, npb.div(cam), bt);
         frustum_point(ct, extra ? bt : nullptr, fr[0], fr[1], fr[2], gx, gy, gz);
+        r = quantize_point(gx, gy, gz, int(npb.div(cam)), o0, o1, o2, d0, d1, d2, n0, n1, n2);
+        if (r >= 0) atomicAdd(&cnt[(unsigned(r) >> shift) & mask], 1);
+        rank[p] = r;
       }
-      r = quantize_point(gx, gy, gz, int(npb.div(cam)), o0, o1, o2, d0, d1, d2, n0, n1, n2);
-      if (r >= 0) atomicAdd(&cnt[(unsigned(r) >> shift) & mask], 1);
-      rank[p] = r;
     }
   }
   __syncthreads();
