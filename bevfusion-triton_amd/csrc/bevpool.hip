@@ -1959,8 +1959,9 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
 // features (S = D*fH*fW, the storage behind the reference's rearrange view,
 // depth_lss.py:94).  Point p = bn*S + s.
 
-// planar -> rows (BN*S, C), fp32.  Vector form (C, S, sbn, sc multiples of 4,
-// 16-byte aligned bases): a block covers 256 consecutive s of one bn; thread
+// planar -> rows (BN*S, C), fp32.  Tiled form (C <= 128, C, S, sbn, sc
+// multiples of 4, 16-byte aligned bases): planar_tile_kernel.  Vector form
+// (wider rows): a block covers 256 consecutive s of one bn; thread
 // (wave w, lane l) owns points s0 + [0, 4) and walks the channels in 4x4
 // blocks c0 + [0, 4) (c0 = 4 (l >> 4) + 16 i): four 16-byte loads along s (16
 // lanes of a channel read 256 contiguous bytes), a register transpose, four
@@ -1978,6 +1979,62 @@ __device__ __forceinline__ void store16(u32x4 *p, u32x4 v) {
 #else
   *p = v;
 #endif
+}
+
+// Tiled planar -> rows: a block moves 64 consecutive s of one bn, all C
+// channels, through an LDS tile [s][C + 1].  Each 16-lane group loads 256
+// contiguous bytes of one channel (kPer = C / 16 rounded up 16-byte loads per
+// thread, all issued before the tile is written); after one barrier the block
+// writes its 64 rows as one contiguous run of 64 * C floats, 16 bytes per
+// thread, consecutive threads at consecutive addresses (non-temporal).
+// Measured at det (1.28 GB): 248 us against 288 us for the register
+// transpose, whose row stores scatter 16-byte pieces over 16 rows.
+template <int kPer>
+__global__ __launch_bounds__(kThreads) void planar_tile_kernel(
+    const float *__restrict__ src, int C, int64_t S, int64_t tiles_s, int64_t sbn, int64_t sc,
+    float *__restrict__ rows) {
+  extern __shared__ float tile[];  // [64][C + 1]
+  const int pitch = C + 1, tid = threadIdx.x;
+  const int64_t bn = int64_t(blockIdx.x) / tiles_s;
+  const int64_t s0 = (int64_t(blockIdx.x) - bn * tiles_s) * 64;
+  const int np = S - s0 < 64 ? int(S - s0) : 64;  // a multiple of 4
+  const float *in = src + bn * sbn + s0;
+  const int npc = C * 16;  // 16-byte pieces on the channel side
+  u32x4 v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    // piece e: channel e / 16, points 4 (e % 16) + [0, 4); pieces past the
+    // tile reload an in-bounds one and are not written
+    const int e = tid + kThreads * i;
+    const int c = e >> 4, pq = e & 15;
+    const int cc = c < C ? c : C - 1, pp = 4 * pq < np ? pq : 0;
+    v[i] = *reinterpret_cast<const u32x4 *>(in + int64_t(cc) * sc + 4 * pp);
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid + kThreads * i;
+    const int c = e >> 4, pq = e & 15;
+    if (e < npc && 4 * pq < np) {
+      float *t = tile + (4 * pq) * pitch + c;
+      t[0] = __uint_as_float(v[i].x);
+      t[pitch] = __uint_as_float(v[i].y);
+      t[2 * pitch] = __uint_as_float(v[i].z);
+      t[3 * pitch] = __uint_as_float(v[i].w);
+    }
+  }
+  __syncthreads();
+  const int q = C >> 2, nrp = np * q;
+  u32x4 *out = reinterpret_cast<u32x4 *>(rows + (bn * S + s0) * C);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid + kThreads * i;  // row e / q, 16-byte column e % q
+    if (e < nrp) {
+      const int p = e / q, j = e - p * q;
+      const float *t = tile + p * pitch + 4 * j;
+      store16(out + e, u32x4{__float_as_uint(t[0]), __float_as_uint(t[1]), __float_as_uint(t[2]),
+                             __float_as_uint(t[3])});
+    }
+  }
 }
 
 template <bool kVec, int kIt>
@@ -2822,7 +2879,22 @@ int bevpool_planar_rows(const float *src, int64_t stride_bn, int64_t stride_c, i
                    reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(rows) % 16 == 0;
   LaunchTimer t("planar_rows", s);
-  if (vec) {
+  if (vec && C <= 128) {
+    const int64_t tiles_s = ceil_div(S, 64);
+    const size_t smem = size_t(64) * size_t(C + 1) * sizeof(float);
+#define BEVPOOL_PT(K)                                                                          \
+  case K:                                                                                      \
+    hipLaunchKernelGGL((planar_tile_kernel<K>), dim3(unsigned(int64_t(BN) * tiles_s)),          \
+                       dim3(kThreads), smem, s, src, C, S, tiles_s, stride_bn, stride_c, rows); \
+    break;
+    switch ((C + 15) / 16) {
+      BEVPOOL_PT(1) BEVPOOL_PT(2) BEVPOOL_PT(3) BEVPOOL_PT(4)
+      BEVPOOL_PT(5) BEVPOOL_PT(6) BEVPOOL_PT(7) BEVPOOL_PT(8)
+      default:
+        return fail(BEVPOOL_EINVAL, "internal: %d channels on the tiled path", C);
+    }
+#undef BEVPOOL_PT
+  } else if (vec) {
     const int64_t tiles_s = ceil_div(S, 256);
     const int passes = (C + 15) / 16;  // 16-channel passes per thread
 #define BEVPOOL_PR(IT)                                                                         \

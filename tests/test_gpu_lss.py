@@ -205,3 +205,25 @@ def test_lss_all_points_dropped(pkg, cuda, synthetic):
     assert int(torch.count_nonzero(out_d)) == 0
     out_d.sum().backward()
     assert int(torch.count_nonzero(depth.grad)) == 0 and int(torch.count_nonzero(context.grad)) == 0
+
+
+@pytest.mark.parametrize('BN,C,S,extra', [
+    (3, 80, 332, 0),       # tiled, last tile of 12 points
+    (2, 4, 68, 0),         # tiled, one 16-byte piece per row
+    (2, 128, 196, 0),      # tiled, widest row
+    (1, 20, 64, 3),        # tiled, channel slice of a wider tensor (channel stride > S)
+    (2, 132, 100, 0),      # wider than the tile: register transpose
+    (2, 6, 50, 0),         # C % 4 != 0: element-wise form
+])
+def test_planar_rows_transpose(pkg, cuda, BN, C, S, extra):
+    """planar (BN, C, S) -> (BN*S, C) rows is an exact copy: compared with
+    torch's permute at partial tiles, every tile width and both fallbacks."""
+    from bevfusion_triton_amd import _pipeline as P
+
+    g = torch.Generator().manual_seed(C + S)
+    wide = torch.randn(BN, C + extra, S, generator=g).to(cuda)
+    src = wide[:, extra:]
+    rows = P.planar_rows(src)
+    torch.cuda.synchronize()
+    exp = src.permute(0, 2, 1).reshape(BN * S, C)
+    assert_bit_equal(rows, exp, f'planar rows BN={BN} C={C} S={S}')
