@@ -144,6 +144,16 @@ int fail(int code, const char *fmt, ...) {
   return code;
 }
 
+// An AQL dispatch carries the grid size in work-items as 32 bits: a launch of
+// more blocks * threads than that is rejected here instead of being
+// truncated (which would leave part of the output unwritten).
+int check_grid(int64_t blocks, int threads, const char *what) {
+  if (blocks < 0 || blocks * int64_t(threads) > int64_t(UINT32_MAX))
+    return fail(BEVPOOL_EINVAL, "%s: %lld blocks of %d threads exceed the 2^32 work-item grid",
+                what, static_cast<long long>(blocks), threads);
+  return BEVPOOL_OK;
+}
+
 int check_launch(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(BEVPOOL_EHIP, "%s: %s", what, hipGetErrorString(e));
@@ -2482,6 +2492,7 @@ int launch_rows_to_bev(const float *acc, int32_t dtype, int C, const int32_t *ce
                        const int32_t *cell_end, int64_t n_cells, int n_z, int64_t n_xy,
                        int64_t out_stride_b, int64_t out_stride_c, int64_t out_stride_z, void *out,
                        hipStream_t s) {
+  if (int st = check_grid(ceil_div(n_cells, kCellTile), kThreads, "cell tiles")) return st;
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
   const int CT = C < kTileChannels ? C : kTileChannels;
   const size_t es = dtype_size(dtype);
@@ -2518,6 +2529,7 @@ int launch_rows_to_bev(const float *acc, int32_t dtype, int C, const int32_t *ce
 int launch_bev_to_rows(const void *grad, size_t es, int64_t gsb, int64_t gsc, int64_t gsz, int C,
                        const int32_t *cell_start, const int32_t *cell_end, int64_t n_cells,
                        int n_z, int64_t n_xy, void *rows, hipStream_t s) {
+  if (int st = check_grid(ceil_div(n_cells, kCellTile), kThreads, "cell tiles")) return st;
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
   const int CT = C < kTileChannels ? C : kTileChannels;
   const size_t smem = size_t(kCellTile) * size_t(CT + 1) * es;
@@ -2879,6 +2891,9 @@ int bevpool_planar_rows(const float *src, int64_t stride_bn, int64_t stride_c, i
                    reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(rows) % 16 == 0;
   LaunchTimer t("planar_rows", s);
+  int st = check_grid(vec ? BN * ceil_div(S, C <= 128 ? 64 : 256) : ceil_div(n_rows * C, kThreads),
+                      kThreads, "planar_rows");
+  if (st) return st;
   if (vec && C <= 128) {
     const int64_t tiles_s = ceil_div(S, 64);
     const size_t smem = size_t(64) * size_t(C + 1) * sizeof(float);
@@ -2938,14 +2953,18 @@ int bevpool_backward_planar(const float *grad, int64_t grad_stride_b, int64_t gr
   if (!scratch || scratch_bytes < bevpool_backward_scratch_bytes(n_cells, C, BEVPOOL_F32))
     return fail(BEVPOOL_ESPACE, "backward scratch too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int st;
-  if ((st = launch_bev_to_rows(grad, 4, grad_stride_b, grad_stride_c, grad_stride_z, C,
-                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
-    return st;
   const bool vec = C % 4 == 0 && S % 4 == 0 && x_stride_bn % 4 == 0 && x_stride_c % 4 == 0 &&
                    reinterpret_cast<uintptr_t>(x_grad) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(rank) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(scratch) % 16 == 0;
+  int st;
+  if ((st = check_grid(vec ? ceil_div(n_points / 4, kThreads) + kXcds
+                           : ceil_div(n_points * C, kThreads),
+                       kThreads, "gather_planar")))
+    return st;
+  if ((st = launch_bev_to_rows(grad, 4, grad_stride_b, grad_stride_c, grad_stride_z, C,
+                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
+    return st;
   const float *g = static_cast<const float *>(scratch);
   LaunchTimer t("gather_planar", s);
   if (vec) {
@@ -3027,6 +3046,7 @@ int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t gra
                 (long long)(2 * int64_t(D) + C));
   hipStream_t s = static_cast<hipStream_t>(stream);
   int st;
+  if ((st = check_grid(ceil_div(n_pix, kDgPix) + kXcds, kThreads, "depth_grad"))) return st;
   if ((st = launch_bev_to_rows(grad, 4, grad_stride_b, grad_stride_c, grad_stride_z, C,
                                cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
     return st;
@@ -3087,12 +3107,11 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                      (reinterpret_cast<uintptr_t>(scratch) % 16 == 0);
   const int vpr = vec16 ? int(row_bytes / 16) : int(C);
   const int64_t total = n_points * vpr;
-  const unsigned grid = xcd_grid(ceil_div(total, int64_t(kThreads) * kGatherPer));
-  const bool narrow = total < (int64_t(1) << 32);
+  const int64_t gather_blocks = ceil_div(total, int64_t(kThreads) * kGatherPer);
   int st;
-  if ((st = launch_bev_to_rows(grad, es, grad_stride_b, grad_stride_c, grad_stride_z, C,
-                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
-    return st;
+  if ((st = check_grid(gather_blocks + kXcds, kThreads, "gather_rows"))) return st;
+  const unsigned grid = xcd_grid(gather_blocks);
+  const bool narrow = total < (int64_t(1) << 32);
   // cache warm-up (gather_warm_block): ranks per XCD + occupied rows
   GatherWarm w{};
   int rank_blocks = 0;
@@ -3113,6 +3132,10 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
   }
   int warm_blocks = rank_blocks + row_blocks;
   warm_blocks = int(ceil_div(warm_blocks, kXcds) * kXcds);  // keep XCD parity
+  if ((st = check_grid(int64_t(grid) + warm_blocks, kThreads, "gather_rows"))) return st;
+  if ((st = launch_bev_to_rows(grad, es, grad_stride_b, grad_stride_c, grad_stride_z, C,
+                               cell_start, cell_end, n_cells, n_z, n_xy, scratch, s)))
+    return st;
   LaunchTimer t("gather_rows", s);
 #define BEVPOOL_GATHER(V, NARROW, LD)                                                          \
   hipLaunchKernelGGL((gather_rows_kernel<V, NARROW>), dim3(grid + unsigned(warm_blocks)),      \

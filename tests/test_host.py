@@ -178,6 +178,12 @@ def test_status_codes_new_entry_points_without_gpu(pkg):
     st = lib.bevpool_planar_rows(p, 1, 1, 1, 0, 4, p, None)
     assert st == -1 and b'planar shape' in lib.bevpool_last_error()
     assert lib.bevpool_planar_rows(p, 1, 1, 0, 4, 4, p, None) == 0  # empty: nothing to do
+    # a launch past the 2^32 work-item grid is refused, not truncated: the
+    # element-wise form (C = 6, 2^30 rows) and the tiled form (1,024 x 2^26 rows)
+    st = lib.bevpool_planar_rows(p, 6 << 30, 1 << 30, 1, 6, 1 << 30, p, None)
+    assert st == -1 and b'work-item grid' in lib.bevpool_last_error()
+    st = lib.bevpool_planar_rows(p, 80 << 26, 1 << 26, 1024, 80, 1 << 26, p, None)
+    assert st == -1 and b'work-item grid' in lib.bevpool_last_error()
     st = lib.bevpool_backward_planar(p, 1, 1, 1, 4, rank.ctypes.data, 10, p, p, 1, 1, 1, 4, p,
                                      1, 1, p, 1 << 20, None)
     assert st == -1 and b'multiple of S' in lib.bevpool_last_error()
