@@ -53,6 +53,7 @@ class QuickCumsumCuda(torch.autograd.Function):
 def bev_pool(feats, coords, B, D, H, W):
     """``bev_pool_legacy.py:99-108``: (B, C, D, H, W) contiguous pooled grid
     of fp32 ``feats`` at (x, y, z, b) ``coords``; gradient to ``feats``."""
+    # the legacy module's own check and exception type (bev_pool_legacy.py:100)
     assert feats.shape[0] == coords.shape[0]
     _require_fp32(feats)
     return BevPoolFunction.apply(feats, coords, int(B), int(D), int(H), int(W))
