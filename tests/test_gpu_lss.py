@@ -227,3 +227,24 @@ def test_planar_rows_transpose(pkg, cuda, BN, C, S, extra):
     torch.cuda.synchronize()
     exp = src.permute(0, 2, 1).reshape(BN * S, C)
     assert_bit_equal(rows, exp, f'planar rows BN={BN} C={C} S={S}')
+
+
+@pytest.mark.parametrize('seed', [11, 12, 13])
+def test_lss_random_rigs(pkg, cuda, synthetic, seed):
+    """Seeded jittered rigs (+-20 deg yaw, +-1 m translation per camera), an
+    off-centre grid with unequal x/y cells and two height bins, 5% of the
+    points pushed out of the grid and points just below its low x edge, on a
+    16 x 44 frustum: indices and fp32 forward/backward bit-exact."""
+    import dataclasses
+
+    spec = dataclasses.replace(
+        synthetic.CASES['det'], image=(128, 352), feature=(16, 44), focal=280.0,
+        yaw_jitter_deg=20.0, trans_jitter_m=1.0, xbound=(-40.0, 56.0, 0.4),
+        ybound=(-60.0, 36.0, 0.32), zbound=(-4.0, 4.0, 4.0), channels=20, oob_fraction=0.05,
+        edge_points=16)
+    geom = synthetic.make_geometry(spec, seed=seed)
+    x = synthetic.make_features(spec, seed=seed)
+    case = synthetic.Case(f'rig{seed}', spec, geom, x, spec.xbound, spec.ybound, spec.zbound)
+    oi = check_index(pkg, case, cuda)
+    assert 0 < int(oi.kept.sum()) < case.n_points
+    check_fwd_bwd(pkg, case, cuda, seed=seed)
