@@ -49,12 +49,19 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_threads() -> int:
+def cpu_threads():
+    """Threads for the CPU baseline and where the figure comes from: the CPU
+    share the environment states for this process (OMP_NUM_THREADS, which the
+    GPU boxes set to their per-GPU share), else every CPU of the process's
+    affinity mask.  Returns (threads, affinity CPUs, source)."""
     try:
-        n = len(os.sched_getaffinity(0))
+        aff = len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        aff = os.cpu_count() or 1
+    env = os.environ.get('OMP_NUM_THREADS', '')
+    if env.isdigit() and int(env) > 0:
+        return min(int(env), aff), aff, 'OMP_NUM_THREADS'
+    return aff, aff, 'affinity'
 
 
 def alg_bytes(n_all, n_kept, n_occ, cells, C, s=4):
@@ -67,21 +74,32 @@ def alg_bytes(n_all, n_kept, n_occ, cells, C, s=4):
 
 
 def kernel_alg_bytes(name, n_all, n_kept, n_occ, cells, C, s=4):
-    """Algorithmic bytes moved by one launch of the named kernel (its share
-    of the path's compulsory traffic plus the index words it must touch)."""
+    """The path's algorithmic bytes (``alg_bytes``) that one launch of the
+    named kernel moves: each compulsory term is charged to the kernel that
+    moves it, and nothing else (sort keys, intermediate cell rows and index
+    words are not algorithmic bytes; see ``kernel_aux_bytes``)."""
     table = {
-        # rows of the kept points (read) + occupied-cell rows (written) + sorted keys
-        'accum_rows': s * C * n_kept + 4 * C * n_occ + 8 * n_kept,
-        # full feature gradient (written) + grad rows of occupied cells + ranks
-        'gather_rows': s * C * n_all + s * C * n_occ + 4 * n_all,
-        # dense BEV (written) + occupied rows (read) + cell ranges
-        'rows_to_bev': s * C * cells + 4 * C * n_occ + 8 * cells,
-        # occupied part of the BEV gradient (read) + rows (written) + cell ranges
-        'bev_to_rows': 2 * s * C * n_occ + 8 * cells,
-        # geometry (read) + ranks (written)
-        'quantize_geom': 12 * n_all + 4 * n_all,
-        # grouped keys (read) + sorted keys (written) + dense cell ranges
-        'bucket_sort': 16 * n_kept + 8 * cells,
+        'accum_rows': s * C * n_kept,     # kept feature rows read
+        'rows_to_bev': s * C * cells,     # dense BEV written
+        'bev_to_rows': s * C * n_occ,     # BEV gradient of occupied cells read
+        'gather_rows': s * C * n_all,     # full feature gradient written
+        'quantize_geom': 12 * n_all,      # geometry read
+    }
+    return table.get(name)
+
+
+def kernel_aux_bytes(name, n_all, n_kept, n_occ, cells, C, s=4):
+    """Bytes a launch must also touch beyond its algorithmic share: index
+    words and the cell-row intermediate between the accumulation and the
+    transposes (reported separately, never in ``roofline.achieved``)."""
+    table = {
+        'accum_rows': 8 * n_kept + 4 * C * n_occ,         # sorted keys + cell rows written
+        'rows_to_bev': 4 * C * n_occ + 8 * cells,         # cell rows read + cell ranges
+        'bev_to_rows': s * C * n_occ + 8 * cells,         # cell rows written + cell ranges
+        'gather_rows': s * C * n_occ + 4 * n_all,         # cell rows read + ranks
+        'quantize_geom': 4 * n_all,                       # ranks written
+        'bucket_sort': 16 * n_kept + 8 * cells,           # keys in / out + cell ranges
+        'radix_scatter': 4 * n_all + 8 * n_kept,          # ranks in, keys out
     }
     return table.get(name)
 
@@ -96,41 +114,54 @@ KERNEL_TIMER_NAMES = (
     ('cell_ranges_kernel', 'cell_ranges'), ('bucket_sort_kernel', 'bucket_sort'),
     ('init_meta', 'init_meta'),
 )
-CALIBRATOR_BYTES = 512 << 20  # the --mode kernels device copy
+CALIBRATOR_BYTES = 512 << 20  # the --mode kernels copy and read-only sum
 
 
 def fold_pmc(fetch_csv, write_csv, config):
     """Fold two ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` runs of
     ``--mode kernels`` into HBM bytes per launch for each library kernel.
 
-    Both counters read in KiB per dispatch.  Each is scaled by the factor that
-    makes the calibrator (a plain 512 MiB device-to-device copy, the largest
-    ``copyBuffer`` dispatches of the run) read exactly 512 MiB and write
-    exactly 512 MiB."""
+    Both counters read in KiB per dispatch.  Two calibrators of known size
+    run at the end of ``--mode kernels``: a plain 512 MiB device-to-device
+    copy (``copyBuffer``: 512 MiB read and 512 MiB written) and a read-only
+    512 MiB sum (``reduce_kernel``: 512 MiB read).  The write counter is
+    scaled by the factor that makes the copy write 512 MiB; the fetch counter
+    by the factor that makes the read-only sum read 512 MiB, and the copy's
+    own fetch factor is reported next to it as a cross-check."""
     import csv
 
     def load(path, counter):
-        per = {}
-        cal = []
+        per, cal = {}, {'copy': [], 'read': []}
         for r in csv.DictReader(open(path)):
             if r['Counter_Name'] != counter:
                 continue
             name, v = r['Kernel_Name'], float(r['Counter_Value'])
             if 'copyBuffer' in name:
-                cal.append(v)
+                cal['copy'].append(v)
+                continue
+            if 'reduce_kernel' in name:
+                cal['read'].append(v)
                 continue
             for dev_name, timer in KERNEL_TIMER_NAMES:
                 if dev_name in name:
                     per.setdefault(timer, []).append(v)
                     break
-        cal = sorted(cal)[-3:]
-        if not cal:
-            raise SystemExit(f'{path}: no calibrator copy dispatches found')
-        factor = (CALIBRATOR_BYTES / 1024) / statistics.mean(cal)
-        return {k: statistics.mean(v) for k, v in per.items()}, factor, statistics.mean(cal)
+        got = {}
+        for k, vals in cal.items():
+            vals = sorted(vals)[-3:]
+            if vals:
+                got[k] = statistics.mean(vals)
+        return {k: statistics.mean(v) for k, v in per.items()}, got
 
-    fetch, ff, fcal = load(fetch_csv, 'FETCH_SIZE')
-    write, wf, wcal = load(write_csv, 'WRITE_SIZE')
+    fetch, fcal = load(fetch_csv, 'FETCH_SIZE')
+    write, wcal = load(write_csv, 'WRITE_SIZE')
+    if 'copy' not in wcal or ('read' not in fcal and 'copy' not in fcal):
+        raise SystemExit('calibrator dispatches (copyBuffer / reduce_kernel) not found')
+    kib = CALIBRATOR_BYTES / 1024
+    ff_copy = kib / fcal['copy'] if 'copy' in fcal else None
+    ff_read = kib / fcal['read'] if 'read' in fcal else None
+    ff = ff_read if ff_read is not None else ff_copy
+    wf = kib / wcal['copy']
     kernels = {}
     for k in sorted(set(fetch) | set(write)):
         f_kib, w_kib = fetch.get(k, 0.0), write.get(k, 0.0)
@@ -138,9 +169,16 @@ def fold_pmc(fetch_csv, write_csv, config):
                       'traffic_bytes': int(round((f_kib * ff + w_kib * wf) * 1024))}
     out = {
         'config': config,
-        'calibration': {'copy_bytes': CALIBRATOR_BYTES, 'fetch_kib': round(fcal, 1),
-                        'write_kib': round(wcal, 1), 'fetch_factor': round(ff, 4),
-                        'write_factor': round(wf, 4)},
+        'calibration': {
+            'bytes': CALIBRATOR_BYTES,
+            'copy_fetch_kib': round(fcal.get('copy', 0.0), 1),
+            'copy_write_kib': round(wcal['copy'], 1),
+            'read_only_fetch_kib': round(fcal.get('read', 0.0), 1),
+            'fetch_factor_read_only': round(ff_read, 4) if ff_read else None,
+            'fetch_factor_copy': round(ff_copy, 4) if ff_copy else None,
+            'fetch_factor_used': round(ff, 4),
+            'write_factor': round(wf, 4),
+        },
         'kernels': kernels,
     }
     path = ROOT / 'profiles' / f'traffic_{config}.json'
@@ -231,6 +269,8 @@ def main():
         src.fill_(1)
         for _ in range(3):
             dst.copy_(src)  # plain copy: 512 MiB read + 512 MiB written per launch
+        for _ in range(3):
+            src.view(torch.float32).sum()  # read-only calibrator: 512 MiB read per launch
         torch.cuda.synchronize()
         log('[bench] kernels mode done')
         return
@@ -309,10 +349,16 @@ def main():
     dom = max(kernels, key=lambda k: kernels[k]['avg_us'] * kernels[k]['launches'])
     dom_us = kernels[dom]['avg_us']
     dom_bytes = kernel_alg_bytes(dom, n_all, n_kept, n_occ, cells, C)
+    dom_aux = kernel_aux_bytes(dom, n_all, n_kept, n_occ, cells, C)
     for name, k in kernels.items():
         b = kernel_alg_bytes(name, n_all, n_kept, n_occ, cells, C)
         if b is not None and k['avg_us'] > 0:
+            k['alg_bytes'] = b
             k['alg_GBps'] = round(b / (k['avg_us'] * 1e-6) / 1e9, 1)
+            k['frac_of_peak'] = round(b / (k['avg_us'] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        a = kernel_aux_bytes(name, n_all, n_kept, n_occ, cells, C)
+        if a is not None:
+            k['aux_bytes'] = a
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9 if dom_bytes else None
 
     # bandwidth calibration: a plain fill and a plain copy of the feature
@@ -382,6 +428,11 @@ def main():
             'frac': round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
             'traffic': traffic,
             'alg_bytes_per_launch': dom_bytes,
+            'alg_bytes_what': 'algorithmic bytes of the path this kernel moves: s*C*N_kept '
+                              'kept feature rows read',
+            'aux_bytes_per_launch': dom_aux,
+            'aux_bytes_what': 'not algorithmic, excluded from achieved: sorted keys read '
+                              '(8*N_kept) + occupied cell rows written (4*C*n_occ)',
             'avg_us': dom_us,
         },
         'op_level': op,
@@ -495,7 +546,9 @@ def config_figure(pkg, lib, name, dev):
 def op_level(pkg, geom, x, module, dev):
     """Op-level bev_pool(feats, coords, B, D, H, W) on the kept points (feats
     (N_kept, C) contiguous, coords int32 (x, y, z, b)): median fwd / bwd over
-    20 back-to-back steps, HIP events; check_bounds off (no host sync)."""
+    20 back-to-back steps, HIP events, for the default call (out-of-grid
+    coordinates reported asynchronously: no host synchronisation) and with
+    check_bounds=False."""
     B = geom.shape[0]
     off, d, nx = module.grid()
     q = ((geom.reshape(B, -1, 3) - torch.tensor(off, device=dev)) /
@@ -508,29 +561,27 @@ def op_level(pkg, geom, x, module, dev):
     feats = x.reshape(B, -1, C)[kept].contiguous().requires_grad_(True)
     X, Y, Z = (int(v) for v in nx)
     g = torch.randn((B, C, Z, X, Y), device=dev)
-
-    def step():
-        out = pkg.bev_pool(feats, coords, B, Z, X, Y, check_bounds=False)
-        torch.autograd.grad(out, feats, g)
-
-    for _ in range(3):
-        step()
-    evs = []
-    for _ in range(20):
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        e[0].record()
-        out = pkg.bev_pool(feats, coords, B, Z, X, Y, check_bounds=False)
-        e[1].record()
-        torch.autograd.grad(out, feats, g)
-        e[2].record()
-        evs.append(e)
-    torch.cuda.synchronize()
-    fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
-    bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
-    return {'what': 'bev_pool(feats (N_kept, C), coords int32) fwd + autograd bwd, median of 20',
-            'n_points': int(feats.shape[0]), 'fwd_us': round(fwd * 1e3, 1),
-            'bwd_us': round(bwd * 1e3, 1),
-            'points_per_s': round(feats.shape[0] / ((fwd + bwd) * 1e-3), 1)}
+    res = {'what': 'bev_pool(feats (N_kept, C), coords int32) fwd + autograd bwd, median of 20',
+           'n_points': int(feats.shape[0])}
+    for label, kw in (('default', {}), ('check_bounds_off', {'check_bounds': False})):
+        for _ in range(3):
+            torch.autograd.grad(pkg.bev_pool(feats, coords, B, Z, X, Y, **kw), feats, g)
+        evs = []
+        for _ in range(20):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record()
+            out = pkg.bev_pool(feats, coords, B, Z, X, Y, **kw)
+            e[1].record()
+            torch.autograd.grad(out, feats, g)
+            e[2].record()
+            evs.append(e)
+        torch.cuda.synchronize()
+        pkg.check_errors()
+        fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+        bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+        res[label] = {'fwd_us': round(fwd * 1e3, 1), 'bwd_us': round(bwd * 1e3, 1),
+                      'points_per_s': round(feats.shape[0] / ((fwd + bwd) * 1e-3), 1)}
+    return res
 
 
 def depth_fused(pkg, geom, module, spec, dev):
@@ -696,7 +747,7 @@ def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1
 
-    threads = cpu_threads()
+    threads, affinity, source = cpu_threads()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     log(f'[bench] cpu baseline, {threads} threads')
@@ -724,6 +775,9 @@ def cpu_baseline(spec, geom_cpu, x_cpu, g_cpu, n_all):
         'value': round(n_all / (fwd + bwd), 1),
         'unit': 'frustum points/s',
         'cores': threads,
+        'threads_source': source,
+        'affinity_cpus': affinity,
+        'os_cpu_count': os.cpu_count(),
         'kind': 'port',
         'sample': f'full det workload ({n_all} points, C=80): torch-CPU restatement of the '
                   f'reference fallback, fwd+bwd, median of {len(runs)} steps (10 s of CPU work) '

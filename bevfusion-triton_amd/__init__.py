@@ -22,7 +22,7 @@ The directory name is not a Python identifier; load it with
 """
 from . import legacy
 from ._lib import BevPoolError, LibraryNotBuilt, library
-from .bev_pool import BevPoolFunction, BevPoolIndexExport, bev_pool
+from .bev_pool import BevPoolFunction, BevPoolIndexExport, bev_pool, check_errors
 from .vtransform import (BevPoolTransform, CameraIndex, LSSIndexExport, create_frustum, gen_dx_bx, host_grid, lss_bev_pool, lss_bev_pool_depth,
                          lss_index_cameras)
 
@@ -35,6 +35,7 @@ __all__ = [
     'LSSIndexExport',
     'LibraryNotBuilt',
     'bev_pool',
+    'check_errors',
     'create_frustum',
     'gen_dx_bx',
     'host_grid',

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime first; see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / 'libbevpool_amd.so'
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F16, BF16 = 0, 1, 2
 META_N_KEPT, META_N_INTERVALS, META_N_BAD, META_FIRST_BAD = 0, 1, 2, 3
@@ -69,9 +69,30 @@ _SIGNATURES = {
     'bevpool_backward_scratch_bytes': ([_i64, _i32, _i32], _sz),
     'bevpool_backward': (
         [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i64, _vp, _i64,
-         _vp, _sz, _vp],
+         _i32, _vp, _sz, _vp],
         ctypes.c_int,
     ),
+    'bevpool_op_workspace_bytes': ([_i64, _i64, _i32], _sz),
+    'bevpool_op_forward': (
+        [_vp, _i32, _i64, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _sz,
+         _vp],
+        ctypes.c_int,
+    ),
+    'bevpool_op_backward': (
+        [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp,
+         _sz, _vp],
+        ctypes.c_int,
+    ),
+    'bevpool_legacy_forward': (
+        [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp],
+        ctypes.c_int,
+    ),
+    'bevpool_legacy_backward': (
+        [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp],
+        ctypes.c_int,
+    ),
+    'bevpool_runs_workspace_bytes': ([_i64], _sz),
+    'bevpool_runs': ([_vp, _i32, _i64, _vp, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
     'bevpool_context_rows': ([_vp, _i64, _i64, _i32, _i32, _i64, _vp, _vp], ctypes.c_int),
     'bevpool_planar_rows': ([_vp, _i64, _i64, _i32, _i32, _i64, _vp, _vp], ctypes.c_int),
     'bevpool_backward_planar': (

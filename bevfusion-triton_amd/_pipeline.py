@@ -278,7 +278,7 @@ def _backward_call(lib, idx, grad, dtype, C, stride_b, stride_c, stride_z, x_gra
         lib.bevpool_backward(
             L.ptr(grad), dtype, stride_b, stride_c, stride_z, C, L.ptr(idx.rank), idx.n_points,
             L.ptr(idx.cell_start), L.ptr(idx.cell_end), idx.B, idx.D, idx.H * idx.W,
-            L.ptr(x_grad), x_grad.stride(0) if idx.n_points else C, L.ptr(scratch),
+            L.ptr(x_grad), x_grad.stride(0) if idx.n_points else C, 1, L.ptr(scratch),
             scratch.numel(), L.stream_handle(idx.device),
         ),
         'bevpool_backward',
@@ -363,4 +363,128 @@ def backward_depth(idx: PoolIndex, grad, C: int, stride_b: int, stride_c: int, s
                 scratch.numel(), L.stream_handle(idx.device),
             ),
             'bevpool_backward_depth',
+        )
+
+
+# ---- deferred (asynchronous) error reports ----------------------------------
+#
+# The device counts invalid inputs (coords outside the grid, intervals outside
+# the arrays) in a meta array.  Reading it at once would synchronise the host
+# with the device on every call; instead the counters are copied to pinned
+# host memory on the call's stream, behind an event, and inspected once that
+# event has completed -- at the next call of the library's autograd
+# functions, or at check_errors().  An error therefore surfaces one call late,
+# the way an asynchronous device error does.
+
+class _Pending:
+    __slots__ = ('event', 'host', 'report')
+
+    def __init__(self, event, host, report):
+        self.event, self.host, self.report = event, host, report
+
+
+_pending = []
+_side_streams = {}
+
+
+def _side_stream(device):
+    """A stream of the library's own per device (default priority) for the
+    counter read-backs, so they never queue behind or ahead of the caller's
+    work on the caller's stream."""
+    s = _side_streams.get(device)
+    if s is None:
+        s = _side_streams[device] = torch.cuda.Stream(device=device)
+    return s
+
+
+def defer_check(meta, report) -> None:
+    """Queue a check of the device counters ``meta`` (int32, written by work
+    already queued on the current stream).  An event marks that point on
+    the caller's stream; the library's side stream waits for it and copies
+    the counters to pinned host memory, so the caller's stream carries only
+    the event.  ``report(host_meta)`` raises if they show an error.  Skipped
+    while the stream is being captured into a graph."""
+    if torch.cuda.is_current_stream_capturing():
+        return
+    device = meta.device
+    host = torch.empty(L.META_LEN, dtype=torch.int32, pin_memory=True)
+    ready = torch.cuda.Event()
+    ready.record()
+    side = _side_stream(device)
+    side.wait_event(ready)
+    with torch.cuda.stream(side):
+        host.copy_(meta[:L.META_LEN], non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+    meta.record_stream(side)  # the allocator keeps meta until the copy has run
+    _pending.append(_Pending(done, host, report))
+
+
+def poll_errors(block: bool = False) -> None:
+    """Raise the first deferred error whose device work has finished (all
+    queued ones when ``block``; that waits for them)."""
+    while _pending:
+        head = _pending[0]
+        if block:
+            head.event.synchronize()
+        elif not head.event.query():
+            return
+        _pending.pop(0)
+        head.report(head.host.numpy())
+
+
+def coords_report(coords, B, D, H, W):
+    """Report of an op-level call: the CPU fallback's ``index_add_`` error
+    (``bev_pool_triton.py:47``) for the first coordinate whose rank lies
+    outside [0, B*D*H*W)."""
+
+    def report(meta):
+        if meta[L.META_N_BAD]:
+            p = int(meta[L.META_FIRST_BAD])
+            x, y, z, b = (int(v) for v in coords[p].tolist())
+            r = ((b * D + z) * H + x) * W + y
+            raise RuntimeError(
+                f'index {r} is out of bounds for dimension 0 with size {B * D * H * W} '
+                f'(point {p}, coords (x={x}, y={y}, z={z}, b={b}); '
+                f'{int(meta[L.META_N_BAD])} such points were excluded)'
+            )
+
+    return report
+
+
+# ---- one-call op level ------------------------------------------------------
+
+def op_workspace(n_points: int, n_cells: int, C: int, device):
+    nbytes = L.library().bevpool_op_workspace_bytes(n_points, n_cells, C)
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def op_meta(ws):
+    """The meta counters at the start of an op-level workspace."""
+    return ws[:4 * L.META_LEN].view(torch.int32)
+
+
+def op_forward(feats2d, coords, B, D, H, W, out, ws) -> None:
+    n, C = feats2d.shape
+    with torch.cuda.device(feats2d.device):
+        L.check(
+            L.library().bevpool_op_forward(
+                L.ptr(feats2d), L.DTYPE_CODES[feats2d.dtype], feats2d.stride(0) if n else C, C,
+                L.ptr(coords), coords.element_size(), coords.stride(0) if n else 4, n, B, D, H,
+                W, L.ptr(out), L.ptr(ws), ws.numel(), L.stream_handle(feats2d.device),
+            ),
+            'bevpool_op_forward',
+        )
+
+
+def op_backward(grad, C, n, B, D, H, W, x_grad, ws, zero_dropped=True) -> None:
+    with torch.cuda.device(grad.device):
+        L.check(
+            L.library().bevpool_op_backward(
+                L.ptr(grad), L.DTYPE_CODES[grad.dtype], grad.stride(0), grad.stride(1),
+                grad.stride(2), C, n, B, D, H, W, L.ptr(x_grad),
+                x_grad.stride(0) if n else C, 1 if zero_dropped else 0, L.ptr(ws), ws.numel(),
+                L.stream_handle(grad.device),
+            ),
+            'bevpool_op_backward',
         )

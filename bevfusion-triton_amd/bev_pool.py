@@ -12,11 +12,15 @@ Differences from the reference, by design:
     bit-identical to the CPU fallback and run-to-run deterministic (the
     reference's Triton path uses unordered atomics, ``:99``); fp16/bf16 inputs
     accumulate in fp32 and round once;
-  * a coordinate whose flattened rank falls outside [0, B*D*H*W) raises the
-    ``RuntimeError`` the CPU fallback's ``index_add_`` raises instead of
-    writing out of bounds (the reference's Triton path does not check); the
-    check synchronises once per call (``check_bounds=False`` skips it -- such
-    points are then ignored);
+  * a coordinate whose flattened rank falls outside [0, B*D*H*W) is excluded
+    on the device instead of being written out of bounds (the reference's
+    Triton path does not check) and reported as the ``RuntimeError`` the CPU
+    fallback's ``index_add_`` raises.  By default the report is asynchronous:
+    the device counters are copied behind an event and the error is raised
+    by the next call of this module's functions once the device has passed
+    that point (or by :func:`check_errors`), so a call never waits for the
+    device.  ``check_bounds='sync'`` waits and raises in the same call;
+    ``check_bounds=False`` drops such points silently;
   * CPU tensors are rejected: the HIP path is the only implementation.
 """
 from __future__ import annotations
@@ -58,49 +62,68 @@ class BevPoolFunction(torch.autograd.Function):
     """Counterpart of ``_BevPoolTritonFunction`` (``bev_pool_triton.py:153-216``):
     forward pools straight into the channel-first (B, C, D, H, W) layout (the
     reference's ``permute().contiguous()`` of ``:227`` is fused into the
-    kernel's store); backward returns ``(x_grad, None x 5)``."""
+    kernel's store) with one call of the library's op-level entry, which
+    leaves the index in its workspace for the backward; backward returns
+    ``(x_grad, None x 6)``."""
 
     @staticmethod
     def forward(ctx, feats, coords, B, D, H, W, check_bounds=True):
         P.require_gpu(feats, coords)
-        C = feats.size(1)
-        ctx.feats_meta = (feats.size(0), C, feats.dtype)
+        P.poll_errors()
+        N, C = feats.shape
+        ctx.feats_meta = (N, C, feats.dtype)
+        ctx.sizes = (B, D, H, W)
         if C == 0:  # nothing to pool; the reference returns an empty (B, 0, D, H, W)
-            ctx.pool_index = None
+            ctx.ws = None
             return feats.new_zeros((B, 0, D, H, W))
-        idx = P.index_from_coords(coords, B, D, H, W)
-        if check_bounds:
-            P.raise_on_bad_coords(idx, coords)
+        P._check_sizes(N, B * D * H * W)
+        feats2d = feats if feats.stride(1) == 1 or N == 0 else feats.contiguous()
+        coords2d = coords if coords.stride(1) == 1 or N == 0 else coords.contiguous()
+        ws = P.op_workspace(N, B * D * H * W, C, feats.device)
         out = torch.empty((B, C, D, H, W), dtype=feats.dtype, device=feats.device)
-        feats2d = feats if feats.stride(1) == 1 or feats.size(0) == 0 else feats.contiguous()
-        P.forward(idx, feats2d, out, C * D * H * W, D * H * W, H * W)
-        ctx.pool_index = idx
+        P.op_forward(feats2d, coords2d, B, D, H, W, out, ws)
+        if check_bounds == 'sync':
+            P.coords_report(coords2d, B, D, H, W)(P.op_meta(ws).cpu().numpy())
+        elif check_bounds:
+            P.defer_check(P.op_meta(ws), P.coords_report(coords2d, B, D, H, W))
+        ctx.ws = ws
         return out
 
     @staticmethod
     def backward(ctx, out_grad):
-        idx = ctx.pool_index
+        P.poll_errors()
         N, C, dtype = ctx.feats_meta
-        if idx is None:
+        B, D, H, W = ctx.sizes
+        if ctx.ws is None:
             return out_grad.new_zeros((N, C), dtype=dtype), None, None, None, None, None, None
         g = out_grad
         if g.dtype != dtype:
             g = g.to(dtype)
-        if g.stride(4) != 1 or g.stride(3) != idx.W:
+        if g.stride(4) != 1 or g.stride(3) != W:
             g = g.contiguous()
         x_grad = torch.empty((N, C), dtype=dtype, device=g.device)
-        P.backward(idx, g, C, g.stride(0), g.stride(1), g.stride(2), x_grad)
+        P.op_backward(g, C, N, B, D, H, W, x_grad, ctx.ws)
         return x_grad, None, None, None, None, None, None
 
 
 def bev_pool(feats: torch.Tensor, coords: torch.Tensor, B: SupportsInt, D: SupportsInt,
-             H: SupportsInt, W: SupportsInt, *, check_bounds: bool = True) -> torch.Tensor:
+             H: SupportsInt, W: SupportsInt, *, check_bounds=True) -> torch.Tensor:
     """``bev_pool_triton.py:219-227``: (N, C) feats + (N, 4) coords (x, y, z, b)
     -> contiguous (B, C, D, H, W).  B, D, H, W may be 0-d integer tensors (the
-    vtransform passes ``self.nx[k]``)."""
+    vtransform passes ``self.nx[k]``).  ``check_bounds``: True (report
+    out-of-grid coords asynchronously, no host synchronisation), ``'sync'``
+    (synchronise and raise in this call) or False."""
     B, D, H, W = int(B), int(D), int(H), int(W)
     _check_inputs(feats, coords, B, D, H, W)
+    if check_bounds not in (True, False, 'sync'):
+        raise ValueError("check_bounds must be True, False or 'sync'")
     return BevPoolFunction.apply(feats, coords, B, D, H, W, check_bounds)
+
+
+def check_errors() -> None:
+    """Wait for the device and raise any deferred error of earlier calls
+    (out-of-grid coordinates, invalid legacy intervals)."""
+    P.poll_errors(block=True)
 
 
 class BevPoolIndexExport:

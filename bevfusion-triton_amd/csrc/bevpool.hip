@@ -1920,7 +1920,7 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const V *__restrict__ rows, int vpr, const int32_t *__restrict__ rank, int64_t n_points,
     V *__restrict__ xg, int64_t xg_ld, int warm_blocks, GatherWarm w,
     const int32_t *__restrict__ cstart, const int32_t *__restrict__ cend, int64_t n_cells,
-    int never) {
+    int never, int zero_dropped) {
   // the first warm_blocks blocks (a multiple of 8, so XCD parity is kept)
   // only pull ranks and rows into the caches ahead of the others
   if (int(blockIdx.x) < warm_blocks) {
@@ -1949,6 +1949,7 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
       const int r = rank[p];
       V v = V{};
       if (r >= 0) v = rows[int64_t(r) * vpr + q];
+      else if (!zero_dropped) continue;  // the caller keeps dropped rows as they are
 #if BEVPOOL_GATHER_NT
       __builtin_nontemporal_store(v, xg + p * xg_ld + q);
 #else
@@ -1956,6 +1957,183 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
 #endif
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// legacy native interface (caller-provided intervals)
+// ---------------------------------------------------------------------------
+
+// Zero bytes [0, n16 * 16) as 16-byte vectors plus a 4-byte tail (n4 words
+// from `tail`), grid-stride.  A kernel rather than a memset so that a graph
+// capture records no memset node.
+__global__ __launch_bounds__(kThreads) void zero_fill_kernel(u32x4 *__restrict__ p, int64_t n16,
+                                                             uint32_t *__restrict__ tail,
+                                                             int64_t n4) {
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n16; i += stride)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) tail[i] = 0u;
+}
+
+// Validates interval j and returns its cell ((b*D + z)*H + x)*W + y from the
+// coordinates of its first row, geom[s] = (x, y, z, b) (the cell of
+// ops/bev_pool/csrc/bev_pool_cuda.cu:33-35), or -1 when its rows [s, s+len)
+// or its cell lie outside the arrays (the reference reads and writes out of
+// bounds there).
+__device__ __forceinline__ int64_t legacy_cell(const int32_t *__restrict__ geom, int64_t n,
+                                               int64_t s, int64_t len, int nb, int nd, int nh,
+                                               int nw) {
+  if (s < 0 || len < 0 || s >= n || s + len > n) return -1;
+  const int gx = geom[4 * s], gy = geom[4 * s + 1], gz = geom[4 * s + 2], gb = geom[4 * s + 3];
+  if (gx < 0 || gx >= nh || gy < 0 || gy >= nw || gz < 0 || gz >= nd || gb < 0 || gb >= nb)
+    return -1;
+  return ((int64_t(gb) * nd + gz) * nh + gx) * nw + gy;
+}
+
+// Interval count: the caller's host count, or min(capacity, device count).
+__device__ __forceinline__ int64_t legacy_count(int64_t cap, const int32_t *__restrict__ dev) {
+  if (!dev) return cap;
+  const int64_t c = *dev;
+  return c < cap ? (c > 0 ? c : 0) : cap;
+}
+
+// ops/bev_pool/csrc/bev_pool_cuda.cu:20-42: interval j sums rows [s, s + len)
+// of x (n, C) -- fp32 from +0.0, rows in order -- and stores the sum to
+// out[cell, :] (channels last).  One wave per interval; lane l owns channels
+// c0 + l + 64 i, so each row is read as one coalesced run; rows are loaded
+// kLegacyBatch at a time before they are added.  Invalid intervals are
+// skipped and counted in meta[BEVPOOL_META_N_BAD] (meta may be null).
+constexpr int kLegacyBatch = 8;
+
+template <int kCPL>
+__global__ __launch_bounds__(kThreads) void legacy_forward_kernel(
+    const float *__restrict__ x, int64_t n, int C, const int32_t *__restrict__ geom,
+    const int32_t *__restrict__ starts, const int32_t *__restrict__ lengths, int64_t cap,
+    const int32_t *__restrict__ count_dev, int nb, int nd, int nh, int nw,
+    float *__restrict__ out, int32_t *__restrict__ meta) {
+  const int64_t n_int = legacy_count(cap, count_dev);
+  const int lane = lane_id();
+  const int64_t nwaves = (int64_t(gridDim.x) * kThreads) >> 6;
+  for (int64_t j = (int64_t(blockIdx.x) * kThreads + threadIdx.x) >> 6; j < n_int; j += nwaves) {
+    const int64_t s = starts[j], len = lengths[j];
+    const int64_t cell = legacy_cell(geom, n, s, len, nb, nd, nh, nw);
+    if (cell < 0) {
+      if (meta && lane == 0) atomicAdd(meta + BEVPOOL_META_N_BAD, 1);
+      continue;
+    }
+    for (int c0 = 0; c0 < C; c0 += 64 * kCPL) {
+      int col[kCPL];
+      float acc[kCPL];
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i) {
+        const int c = c0 + lane + 64 * i;
+        col[i] = c < C ? c : C - 1;  // lanes past C read a valid column, store nothing
+        acc[i] = 0.0f;
+      }
+      for (int64_t r0 = 0; r0 < len; r0 += kLegacyBatch) {
+        float v[kLegacyBatch][kCPL];
+#pragma unroll
+        for (int u = 0; u < kLegacyBatch; ++u) {
+          const int64_t r = s + (r0 + u < len ? r0 + u : 0);
+#pragma unroll
+          for (int i = 0; i < kCPL; ++i) v[u][i] = x[r * C + col[i]];
+        }
+#pragma unroll
+        for (int u = 0; u < kLegacyBatch; ++u)
+          if (r0 + u < len)
+#pragma unroll
+            for (int i = 0; i < kCPL; ++i) acc[i] += v[u][i];
+      }
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i)
+        if (c0 + lane + 64 * i < C) out[cell * C + c0 + lane + 64 * i] = acc[i];
+    }
+  }
+}
+
+// ops/bev_pool/csrc/bev_pool_cuda.cu:61-84: every row of interval j gets the
+// gradient row of its cell, x_grad[r, :] = g[cell, :] (g channels last).  One
+// wave per interval, lanes over channels as in the forward.
+template <int kCPL>
+__global__ __launch_bounds__(kThreads) void legacy_backward_kernel(
+    const float *__restrict__ g, int64_t n, int C, const int32_t *__restrict__ geom,
+    const int32_t *__restrict__ starts, const int32_t *__restrict__ lengths, int64_t cap,
+    const int32_t *__restrict__ count_dev, int nb, int nd, int nh, int nw,
+    float *__restrict__ xg, int32_t *__restrict__ meta) {
+  const int64_t n_int = legacy_count(cap, count_dev);
+  const int lane = lane_id();
+  const int64_t nwaves = (int64_t(gridDim.x) * kThreads) >> 6;
+  for (int64_t j = (int64_t(blockIdx.x) * kThreads + threadIdx.x) >> 6; j < n_int; j += nwaves) {
+    const int64_t s = starts[j], len = lengths[j];
+    const int64_t cell = legacy_cell(geom, n, s, len, nb, nd, nh, nw);
+    if (cell < 0) {
+      if (meta && lane == 0) atomicAdd(meta + BEVPOOL_META_N_BAD, 1);
+      continue;
+    }
+    for (int c0 = 0; c0 < C; c0 += 64 * kCPL) {
+      float v[kCPL];
+#pragma unroll
+      for (int i = 0; i < kCPL; ++i) {
+        const int c = c0 + lane + 64 * i;
+        v[i] = g[cell * C + (c < C ? c : C - 1)];
+      }
+      for (int64_t r = s; r < s + len; ++r)
+#pragma unroll
+        for (int i = 0; i < kCPL; ++i)
+          if (c0 + lane + 64 * i < C) xg[r * C + c0 + lane + 64 * i] = v[i];
+    }
+  }
+}
+
+// Run boundaries of a rank array (ops/bev_pool/bev_pool_legacy.py:56-61:
+// flag[0] = 1, flag[i] = rank[i] != rank[i-1]).  Per block of 256 positions:
+// the number of run starts.
+template <typename TR>
+__global__ __launch_bounds__(kThreads) void run_count_kernel(const TR *__restrict__ ranks,
+                                                             int64_t n,
+                                                             int32_t *__restrict__ bcount) {
+  __shared__ int s_w[kWaves];
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const bool is_start = i < n && (i == 0 || ranks[i] != ranks[i - 1]);
+  const uint64_t b = __ballot(is_start);
+  if (lane_id() == 0) s_w[threadIdx.x >> 6] = __popcll(b);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int s = 0;
+    for (int j = 0; j < kWaves; ++j) s += s_w[j];
+    bcount[blockIdx.x] = s;
+  }
+}
+
+// Run starts in order, at the block offsets scanned from run_count_kernel.
+template <typename TR>
+__global__ __launch_bounds__(kThreads) void run_write_kernel(const TR *__restrict__ ranks,
+                                                             int64_t n,
+                                                             const int32_t *__restrict__ boff,
+                                                             int32_t *__restrict__ starts) {
+  __shared__ int s_w[kWaves];
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int w = threadIdx.x >> 6;
+  const bool is_start = i < n && (i == 0 || ranks[i] != ranks[i - 1]);
+  const uint64_t b = __ballot(is_start);
+  if (lane_id() == 0) s_w[w] = __popcll(b);
+  __syncthreads();
+  if (is_start) {
+    int off = boff[blockIdx.x] + __popcll(b & lanes_below());
+    for (int j = 0; j < w; ++j) off += s_w[j];
+    starts[off] = int(i);
+  }
+}
+
+// lengths[j] = starts[j + 1] - starts[j], the last one n - starts[j]
+// (bev_pool_legacy.py:58-61), for the count(meta) runs.
+__global__ __launch_bounds__(kThreads) void run_length_kernel(const int32_t *__restrict__ starts,
+                                                              int64_t n,
+                                                              const int32_t *__restrict__ count,
+                                                              int32_t *__restrict__ lengths) {
+  const int64_t m = *count;
+  const int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (j < m) lengths[j] = int((j + 1 < m ? int64_t(starts[j + 1]) : n) - starts[j]);
 }
 
 // ---------------------------------------------------------------------------
@@ -2557,6 +2735,76 @@ int launch_bev_to_rows(const void *grad, size_t es, int64_t gsb, int64_t gsc, in
   return check_launch("bev_to_rows");
 }
 
+// Zero `bytes` bytes at p (4-byte aligned, a multiple of 4 bytes) with
+// zero_fill_kernel.
+int launch_zero_fill(void *p, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return BEVPOOL_OK;
+  const bool vec = reinterpret_cast<uintptr_t>(p) % 16 == 0;
+  const int64_t n16 = vec ? int64_t(bytes / 16) : 0;
+  const int64_t n4 = int64_t((bytes - size_t(n16) * 16) / 4);
+  const int64_t items = n16 > n4 ? n16 : n4;
+  const int64_t blocks = ceil_div(items, kThreads) < 4096 ? ceil_div(items, kThreads) : 4096;
+  LaunchTimer t("zero_fill", s);
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+                     static_cast<u32x4 *>(p), n16,
+                     reinterpret_cast<uint32_t *>(static_cast<char *>(p) + n16 * 16), n4);
+  return check_launch("zero_fill");
+}
+
+// Channels per lane of the legacy kernels: 1 (C <= 64), 2 (<= 128), else 4
+// (with a loop over 256-channel blocks).
+int legacy_cpl(int C) { return C <= 64 ? 1 : (C <= 128 ? 2 : 4); }
+
+unsigned legacy_grid(int64_t cap) {
+  const int64_t b = ceil_div(cap, kWaves);
+  return unsigned(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+int check_legacy_args(int64_t n, int32_t C, const void *geom, const void *starts,
+                      const void *lengths, int64_t n_intervals, int32_t b, int32_t d, int32_t h,
+                      int32_t w, const void *out) {
+  if (n < 0 || n > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "n=%lld out of range", (long long)n);
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (b < 1 || d < 1 || h < 1 || w < 1)
+    return fail(BEVPOOL_EINVAL, "b, d, h, w must be positive");
+  if (int64_t(b) * d * h * w > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "b*d*h*w exceeds 2^31-1");
+  if (n_intervals < 0 || n_intervals > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_intervals out of range");
+  if (!out) return fail(BEVPOOL_EINVAL, "null output");
+  if (n_intervals > 0 && (!geom || !starts || !lengths))
+    return fail(BEVPOOL_EINVAL, "null geom_feats / interval arrays");
+  return BEVPOOL_OK;
+}
+
+// Layout of the op-level workspace (bevpool_op_forward / bevpool_op_backward):
+// meta, the index (ranks, sorted keys, cell ranges), the index-stage
+// workspace and the cell-row scratch shared by the forward and the backward.
+struct OpLayout {
+  size_t meta, rank, keys, cstart, cend, index_ws, scratch, total;
+};
+
+OpLayout op_layout(int64_t n, int64_t cells, int32_t C) {
+  OpLayout L;
+  size_t o = 0;
+  L.meta = o;
+  o = align256(o + BEVPOOL_META_LEN * sizeof(int32_t));
+  L.rank = o;
+  o = align256(o + size_t(n) * sizeof(int32_t));
+  L.keys = o;
+  o = align256(o + size_t(n) * sizeof(uint64_t));
+  L.cstart = o;
+  o = align256(o + size_t(cells) * sizeof(int32_t));
+  L.cend = o;
+  o = align256(o + size_t(cells) * sizeof(int32_t));
+  L.index_ws = o;
+  o = align256(o + index_layout(n).total);
+  L.scratch = o;
+  o = align256(o + size_t(cells) * size_t(C) * sizeof(float));
+  L.total = o;
+  return L;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -3081,8 +3329,8 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                      int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
                      const int32_t *rank, int64_t n_points, const int32_t *cell_start,
                      const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
-                     void *x_grad, int64_t x_grad_row_stride, void *scratch,
-                     size_t scratch_bytes, void *stream) {
+                     void *x_grad, int64_t x_grad_row_stride, int32_t zero_dropped,
+                     void *scratch, size_t scratch_bytes, void *stream) {
   g_last_error.clear();
   if (dtype != BEVPOOL_F32 && dtype != BEVPOOL_F16 && dtype != BEVPOOL_BF16)
     return fail(BEVPOOL_EINVAL, "unsupported dtype code %d", dtype);
@@ -3141,7 +3389,7 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
   hipLaunchKernelGGL((gather_rows_kernel<V, NARROW>), dim3(grid + unsigned(warm_blocks)),      \
                      dim3(kThreads), 0, s, static_cast<const V *>(scratch), vpr, rank,        \
                      n_points, static_cast<V *>(x_grad), LD, warm_blocks, w, cell_start,     \
-                     cell_end, n_cells, 0)
+                     cell_end, n_cells, 0, zero_dropped ? 1 : 0)
   if (vec16) {
     const int64_t ld = int64_t(size_t(x_grad_row_stride) * es / 16);
     if (narrow) BEVPOOL_GATHER(u32x4, true, ld); else BEVPOOL_GATHER(u32x4, false, ld);
@@ -3154,6 +3402,186 @@ int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
   }
 #undef BEVPOOL_GATHER
   return check_launch("gather_rows");
+}
+
+int bevpool_legacy_forward(const float *x, int64_t n, int32_t C, const int32_t *geom_feats,
+                           const int32_t *interval_starts, const int32_t *interval_lengths,
+                           int64_t n_intervals, const int32_t *n_intervals_dev, int32_t b,
+                           int32_t d, int32_t h, int32_t w, float *out, int32_t *meta,
+                           void *stream) {
+  g_last_error.clear();
+  int st = check_legacy_args(n, C, geom_feats, interval_starts, interval_lengths, n_intervals, b,
+                             d, h, w, out);
+  if (st) return st;
+  if (n_intervals > 0 && n > 0 && !x) return fail(BEVPOOL_EINVAL, "null x");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t cells = int64_t(b) * d * h * w;
+  if ((st = launch_zero_fill(out, size_t(cells) * size_t(C) * sizeof(float), s))) return st;
+  if (n_intervals == 0) return BEVPOOL_OK;
+  LaunchTimer t("legacy_forward", s);
+#define BEVPOOL_LF(K)                                                                          \
+  hipLaunchKernelGGL((legacy_forward_kernel<K>), dim3(legacy_grid(n_intervals)), dim3(kThreads), \
+                     0, s, x, n, C, geom_feats, interval_starts, interval_lengths, n_intervals,  \
+                     n_intervals_dev, b, d, h, w, out, meta)
+  switch (legacy_cpl(C)) {
+    case 1: BEVPOOL_LF(1); break;
+    case 2: BEVPOOL_LF(2); break;
+    default: BEVPOOL_LF(4); break;
+  }
+#undef BEVPOOL_LF
+  return check_launch("legacy_forward");
+}
+
+int bevpool_legacy_backward(const float *out_grad, int64_t n, int32_t C,
+                            const int32_t *geom_feats, const int32_t *interval_starts,
+                            const int32_t *interval_lengths, int64_t n_intervals,
+                            const int32_t *n_intervals_dev, int32_t b, int32_t d, int32_t h,
+                            int32_t w, float *x_grad, int32_t *meta, void *stream) {
+  g_last_error.clear();
+  int st = check_legacy_args(n, C, geom_feats, interval_starts, interval_lengths, n_intervals, b,
+                             d, h, w, n > 0 ? x_grad : reinterpret_cast<float *>(1));
+  if (st) return st;
+  if (n_intervals > 0 && !out_grad) return fail(BEVPOOL_EINVAL, "null out_grad");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((st = launch_zero_fill(x_grad, size_t(n) * size_t(C) * sizeof(float), s))) return st;
+  if (n_intervals == 0 || n == 0) return BEVPOOL_OK;
+  LaunchTimer t("legacy_backward", s);
+#define BEVPOOL_LB(K)                                                                          \
+  hipLaunchKernelGGL((legacy_backward_kernel<K>), dim3(legacy_grid(n_intervals)),              \
+                     dim3(kThreads), 0, s, out_grad, n, C, geom_feats, interval_starts,        \
+                     interval_lengths, n_intervals, n_intervals_dev, b, d, h, w, x_grad, meta)
+  switch (legacy_cpl(C)) {
+    case 1: BEVPOOL_LB(1); break;
+    case 2: BEVPOOL_LB(2); break;
+    default: BEVPOOL_LB(4); break;
+  }
+#undef BEVPOOL_LB
+  return check_launch("legacy_backward");
+}
+
+size_t bevpool_runs_workspace_bytes(int64_t n) {
+  if (n < 0) return 0;
+  return align256(size_t(ceil_div(n, kThreads) + 1) * sizeof(int32_t));
+}
+
+int bevpool_runs(const void *ranks, int32_t rank_bytes, int64_t n, int32_t *starts,
+                 int32_t *lengths, int32_t *meta, void *workspace, size_t workspace_bytes,
+                 void *stream) {
+  g_last_error.clear();
+  if (rank_bytes != 4 && rank_bytes != 8)
+    return fail(BEVPOOL_EINVAL, "rank_bytes must be 4 or 8, got %d", rank_bytes);
+  if (n < 0 || n > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "n out of range");
+  if (!meta || !workspace) return fail(BEVPOOL_EINVAL, "null meta or workspace");
+  if (workspace_bytes < bevpool_runs_workspace_bytes(n))
+    return fail(BEVPOOL_ESPACE, "runs workspace %zu bytes < required %zu", workspace_bytes,
+                bevpool_runs_workspace_bytes(n));
+  if (n > 0 && (!ranks || !starts || !lengths))
+    return fail(BEVPOOL_EINVAL, "null ranks / starts / lengths");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int st;
+  {
+    LaunchTimer t("init_meta", s);
+    hipLaunchKernelGGL(init_meta_kernel, dim3(1), dim3(64), 0, s, meta);
+    if ((st = check_launch("init_meta"))) return st;
+  }
+  if (n == 0) return BEVPOOL_OK;
+  const int64_t blocks = ceil_div(n, kThreads);
+  if ((st = check_grid(blocks, kThreads, "runs"))) return st;
+  int32_t *bcount = static_cast<int32_t *>(workspace);
+  {
+    LaunchTimer t("run_count", s);
+    if (rank_bytes == 4)
+      hipLaunchKernelGGL(run_count_kernel<int32_t>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+                         static_cast<const int32_t *>(ranks), n, bcount);
+    else
+      hipLaunchKernelGGL(run_count_kernel<int64_t>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+                         static_cast<const int64_t *>(ranks), n, bcount);
+    if ((st = check_launch("run_count"))) return st;
+  }
+  {
+    LaunchTimer t("scan_counts", s);
+    hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(kThreads), 0, s, bcount, blocks,
+                       meta + BEVPOOL_META_N_INTERVALS);
+    if ((st = check_launch("scan_counts"))) return st;
+  }
+  {
+    LaunchTimer t("run_write", s);
+    if (rank_bytes == 4)
+      hipLaunchKernelGGL(run_write_kernel<int32_t>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+                         static_cast<const int32_t *>(ranks), n, bcount, starts);
+    else
+      hipLaunchKernelGGL(run_write_kernel<int64_t>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+                         static_cast<const int64_t *>(ranks), n, bcount, starts);
+    if ((st = check_launch("run_write"))) return st;
+  }
+  LaunchTimer t("run_length", s);
+  hipLaunchKernelGGL(run_length_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, s, starts, n,
+                     meta + BEVPOOL_META_N_INTERVALS, lengths);
+  return check_launch("run_length");
+}
+
+size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C) {
+  if (n_points < 0 || n_cells < 0 || C < 0) return 0;
+  return op_layout(n_points, n_cells, C).total;
+}
+
+int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                       const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
+                       int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W, void *out,
+                       void *workspace, size_t workspace_bytes, void *stream) {
+  g_last_error.clear();
+  if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range", (long long)n_points);
+  const int64_t cells = int64_t(B) * D * H * W;
+  if (cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "B*D*H*W exceeds 2^31-1");
+  if (!workspace) return fail(BEVPOOL_EINVAL, "null workspace");
+  const OpLayout L = op_layout(n_points, cells, C);
+  if (workspace_bytes < L.total)
+    return fail(BEVPOOL_ESPACE, "op workspace %zu bytes < required %zu", workspace_bytes, L.total);
+  char *ws = static_cast<char *>(workspace);
+  int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
+  int32_t *rank = reinterpret_cast<int32_t *>(ws + L.rank);
+  uint64_t *keys = reinterpret_cast<uint64_t *>(ws + L.keys);
+  int32_t *cstart = reinterpret_cast<int32_t *>(ws + L.cstart);
+  int32_t *cend = reinterpret_cast<int32_t *>(ws + L.cend);
+  void *iws = ws + L.index_ws;
+  const size_t iws_bytes = index_layout(n_points).total;
+  int st = bevpool_coord_ranks(coords, coord_bytes, n_points, coords_row_stride, B, D, H, W,
+                               rank, meta, iws, iws_bytes, stream);
+  if (st) return st;
+  if ((st = bevpool_sort(rank, n_points, cells, keys, cstart, cend, meta, iws, iws_bytes, stream)))
+    return st;
+  const int64_t hw = int64_t(H) * W;
+  return bevpool_forward(feats, dtype, feats_row_stride, C, n_points, keys, cstart, cend, meta, B,
+                         D, hw, int64_t(C) * D * hw, int64_t(D) * hw, hw, out, ws + L.scratch,
+                         size_t(cells) * size_t(C) * sizeof(float), stream);
+}
+
+int bevpool_op_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
+                        int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
+                        int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W,
+                        void *x_grad, int64_t x_grad_row_stride, int32_t zero_dropped,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+  g_last_error.clear();
+  if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range", (long long)n_points);
+  const int64_t cells = int64_t(B) * D * H * W;
+  if (cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "B*D*H*W exceeds 2^31-1");
+  if (!workspace) return fail(BEVPOOL_EINVAL, "null workspace");
+  const OpLayout L = op_layout(n_points, cells, C);
+  if (workspace_bytes < L.total)
+    return fail(BEVPOOL_ESPACE, "op workspace %zu bytes < required %zu", workspace_bytes, L.total);
+  char *ws = static_cast<char *>(workspace);
+  return bevpool_backward(grad, dtype, grad_stride_b, grad_stride_c, grad_stride_z, C,
+                          reinterpret_cast<const int32_t *>(ws + L.rank), n_points,
+                          reinterpret_cast<const int32_t *>(ws + L.cstart),
+                          reinterpret_cast<const int32_t *>(ws + L.cend), B, D, int64_t(H) * W,
+                          x_grad, x_grad_row_stride, zero_dropped, ws + L.scratch,
+                          size_t(cells) * size_t(C) * dtype_size(dtype), stream);
 }
 
 int bevpool_timing_enable(int enable) {

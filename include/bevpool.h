@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define BEVPOOL_ABI_VERSION 1
+#define BEVPOOL_ABI_VERSION 2
 
 /* status codes */
 #define BEVPOOL_OK 0
@@ -223,14 +223,17 @@ size_t bevpool_backward_scratch_bytes(int64_t n_cells, int32_t C, int32_t dtype)
  *   grad         dtype; element (b, c, z, xy) at
  *                b*grad_stride_b + c*grad_stride_c + z*grad_stride_z + xy
  *   x_grad       out: dtype [n_points, C], row stride x_grad_row_stride
+ *   zero_dropped 1: rows of dropped points (rank -1) are written as zero (the
+ *                zero-filled gradient of base.py:157's kept-mask gather);
+ *                0: those rows are left untouched
  *   scratch      >= bevpool_backward_scratch_bytes(n_cells, C, dtype) bytes
  */
 int bevpool_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                      int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
                      const int32_t *rank, int64_t n_points, const int32_t *cell_start,
                      const int32_t *cell_end, int32_t n_batch, int32_t n_z, int64_t n_xy,
-                     void *x_grad, int64_t x_grad_row_stride, void *scratch,
-                     size_t scratch_bytes, void *stream);
+                     void *x_grad, int64_t x_grad_row_stride, int32_t zero_dropped,
+                     void *scratch, size_t scratch_bytes, void *stream);
 
 /*
  * Planar (channel-first) camera features.  The reference's features are the
@@ -333,6 +336,94 @@ int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t gra
                            float *grad_depth, float *grad_context, int64_t gctx_stride_bn,
                            int64_t gctx_stride_c, void *scratch, size_t scratch_bytes,
                            void *stream);
+
+/*
+ * One-call op level: ops/bev_pool/src/bev_pool_triton.py:219-227
+ * (bev_pool(feats, coords, B, D, H, W)) as bevpool_coord_ranks ->
+ * bevpool_sort -> bevpool_forward on one caller-owned workspace, which keeps
+ * the index (ranks, sorted keys, cell ranges) for bevpool_op_backward.
+ * The workspace starts with the BEVPOOL_META_LEN int32 meta counters
+ * (meta[BEVPOOL_META_N_BAD] = points whose rank falls outside [0, B*D*H*W):
+ * they are excluded, where the reference CPU fallback raises).  One
+ * workspace serves one forward/backward pair at a time.
+ *
+ *   feats        dtype [n_points, C], row stride feats_row_stride, channel stride 1
+ *   coords       int32 / int64 (coord_bytes 4 / 8) [n_points, 4] (x, y, z, b)
+ *   out          dtype, contiguous (B, C, D, H, W)
+ */
+size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C);
+
+int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                       const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
+                       int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W, void *out,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Backward of bevpool_op_forward (bev_pool_triton.py:189-216): x_grad[p, :]
+ * = grad at p's cell, on the index the last bevpool_op_forward left in the
+ * workspace.  grad element (b, c, z, xy) at b*grad_stride_b + c*grad_stride_c
+ * + z*grad_stride_z + xy (xy = x*W + y contiguous); zero_dropped as
+ * bevpool_backward.
+ */
+int bevpool_op_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
+                        int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
+                        int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W,
+                        void *x_grad, int64_t x_grad_row_stride, int32_t zero_dropped,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Legacy native interface: the reference's pybind extension functions
+ * bev_pool_forward / bev_pool_backward (ops/bev_pool/csrc/bev_pool_cpu.cpp:22-94,
+ * kernels ops/bev_pool/csrc/bev_pool_cuda.cu:20-98), called by
+ * ops/bev_pool/bev_pool_legacy.py:64-73, 85-94.  Intervals are caller-given
+ * runs of rows: interval j covers rows [interval_starts[j],
+ * interval_starts[j] + interval_lengths[j]) of x, and its cell is
+ * geom_feats[interval_starts[j]] = (x, y, z, b).
+ *
+ * Forward: out (b, d, h, w, C) fp32 contiguous is zero-filled, then
+ * out[cell, :] = the sum of the interval's rows, fp32 from +0.0 in row order
+ * (the reference kernel's psum loop).  Backward: x_grad (n, C) fp32 is
+ * zero-filled, then every row of an interval gets out_grad[cell, :]
+ * (out_grad (b, d, h, w, C) contiguous).  Two intervals of one cell race as
+ * in the reference.
+ *
+ * Differences from the reference: an interval whose rows or cell fall outside
+ * the arrays is skipped and counted in meta[BEVPOOL_META_N_BAD] (meta may be
+ * NULL) instead of reading/writing out of bounds; the interval count is
+ * n_intervals, or, when n_intervals_dev is not NULL, min(n_intervals,
+ * *n_intervals_dev) read on the device (capacity + device count, so a caller
+ * chaining bevpool_runs needs no host synchronisation).  The caller passes
+ * the arrays in the reference's argument order (lengths before starts in the
+ * Python wrapper, starts before lengths in the kernel; here starts first).
+ *   x, geom_feats, out_grad: contiguous; interval arrays int32.
+ */
+int bevpool_legacy_forward(const float *x, int64_t n, int32_t C, const int32_t *geom_feats,
+                           const int32_t *interval_starts, const int32_t *interval_lengths,
+                           int64_t n_intervals, const int32_t *n_intervals_dev, int32_t b,
+                           int32_t d, int32_t h, int32_t w, float *out, int32_t *meta,
+                           void *stream);
+
+int bevpool_legacy_backward(const float *out_grad, int64_t n, int32_t C,
+                            const int32_t *geom_feats, const int32_t *interval_starts,
+                            const int32_t *interval_lengths, int64_t n_intervals,
+                            const int32_t *n_intervals_dev, int32_t b, int32_t d, int32_t h,
+                            int32_t w, float *x_grad, int32_t *meta, void *stream);
+
+/*
+ * Runs of equal values in a rank array (int32 or int64, rank_bytes 4 / 8):
+ * ops/bev_pool/bev_pool_legacy.py:56-61 (start flags rank[i] != rank[i-1],
+ * interval_starts = where(flags), lengths by difference, the last n - start)
+ * without torch.where's host synchronisation.
+ *   starts, lengths   out: int32 [n] (capacity); the first
+ *                     meta[BEVPOOL_META_N_INTERVALS] entries are written
+ *   meta              int32 [BEVPOOL_META_LEN], reset by this call
+ *   workspace         >= bevpool_runs_workspace_bytes(n)
+ */
+size_t bevpool_runs_workspace_bytes(int64_t n);
+
+int bevpool_runs(const void *ranks, int32_t rank_bytes, int64_t n, int32_t *starts,
+                 int32_t *lengths, int32_t *meta, void *workspace, size_t workspace_bytes,
+                 void *stream);
 
 /*
  * Optional per-kernel timing.  When enabled, every kernel launch is bracketed

@@ -258,3 +258,76 @@ def lss_index(geom_feats, dx, bx, nx) -> LSSIndex:
     sorted_ranks = rk[order]
     starts, lengths = intervals(sorted_ranks)
     return LSSIndex(rank, q.kept, perm, sorted_ranks, starts, lengths)
+
+
+# ---------------------------------------------------------------------------
+# legacy extension: ops/bev_pool/csrc/bev_pool_cpu.cpp:22-94 and the kernels
+# of ops/bev_pool/csrc/bev_pool_cuda.cu:20-98, driven by
+# ops/bev_pool/bev_pool_legacy.py:53-96
+# ---------------------------------------------------------------------------
+def legacy_cell(geom_feats, s, b, d, h, w):
+    """Cell of the interval starting at row s (``bev_pool_cuda.cu:33-35``:
+    ((gb*d + gz)*h + gx)*w + gy from geom_feats[s] = (gx, gy, gz, gb)), or
+    None when the row or the cell lies outside the arrays (the reference
+    reads / writes out of bounds there; the library skips the interval)."""
+    if s < 0 or s >= geom_feats.shape[0]:
+        return None
+    gx, gy, gz, gb = (int(v) for v in geom_feats[s])
+    if not (0 <= gx < h and 0 <= gy < w and 0 <= gz < d and 0 <= gb < b):
+        return None
+    return ((gb * d + gz) * h + gx) * w + gy
+
+
+def _valid_interval(s, n_rows, n):
+    return 0 <= s and 0 <= n_rows and s < n and s + n_rows <= n
+
+
+def legacy_forward(x, geom_feats, interval_lengths, interval_starts, b, d, h, w):
+    """``bev_pool_forward`` (``bev_pool_cpu.cpp:22-47`` + ``bev_pool_cuda.cu:20-42``):
+    zeros (b, d, h, w, c); interval j stores psum = ((0 + x[s]) + x[s+1]) + ...
+    (fp32, rows in order) at the cell of its first row.  Returns (out, n_bad)
+    with n_bad the intervals skipped as invalid."""
+    n, c = x.shape
+    out = torch.zeros((b * d * h * w, c), dtype=torch.float32)
+    n_bad = 0
+    for j in range(int(interval_lengths.shape[0])):
+        s, m = int(interval_starts[j]), int(interval_lengths[j])
+        cell = legacy_cell(geom_feats, s, b, d, h, w) if _valid_interval(s, m, n) else None
+        if cell is None:
+            n_bad += 1
+            continue
+        psum = torch.zeros(c, dtype=torch.float32)
+        for i in range(m):
+            psum = psum + x[s + i]
+        out[cell] = psum
+    return out.view(b, d, h, w, c), n_bad
+
+
+def legacy_backward(out_grad, geom_feats, interval_lengths, interval_starts, b, d, h, w):
+    """``bev_pool_backward`` (``bev_pool_cpu.cpp:60-87`` + ``bev_pool_cuda.cu:61-84``):
+    zeros (n, c), n = geom_feats rows; every row of interval j gets
+    out_grad[cell]."""
+    n, c = geom_feats.shape[0], out_grad.shape[4]
+    g = out_grad.reshape(b * d * h * w, c)
+    x_grad = torch.zeros((n, c), dtype=torch.float32)
+    n_bad = 0
+    for j in range(int(interval_lengths.shape[0])):
+        s, m = int(interval_starts[j]), int(interval_lengths[j])
+        cell = legacy_cell(geom_feats, s, b, d, h, w) if _valid_interval(s, m, n) else None
+        if cell is None:
+            n_bad += 1
+            continue
+        x_grad[s:s + m] = g[cell]
+    return x_grad, n_bad
+
+
+def runs(ranks):
+    """``bev_pool_legacy.py:56-61`` on any rank array (not necessarily sorted):
+    the same as :func:`intervals`."""
+    return intervals(ranks)
+
+
+def legacy_ranks(coords, B, D, H, W):
+    """``bev_pool_legacy.py:102``: x*(W*D*B) + y*(D*B) + z*B + b."""
+    c = coords.long()
+    return c[:, 0] * (W * D * B) + c[:, 1] * (D * B) + c[:, 2] * B + c[:, 3]

@@ -248,3 +248,33 @@ def test_lss_random_rigs(pkg, cuda, synthetic, seed):
     oi = check_index(pkg, case, cuda)
     assert 0 < int(oi.kept.sum()) < case.n_points
     check_fwd_bwd(pkg, case, cuda, seed=seed)
+
+
+@pytest.mark.parametrize('dtype,autocast', [(torch.bfloat16, False), (torch.float16, False),
+                                            (torch.bfloat16, True)])
+def test_force_fp32_half_inputs(pkg, cuda, synthetic, dtype, autocast):
+    """``@force_fp32`` on ``BaseTransform.bev_pool`` (models/helper/amp.py:35-67,
+    models/vtransforms/base.py:131): half-precision x and geometry are cast
+    to fp32 and pooled with autocast disabled, at the det shape.  The output
+    is fp32 and bit-exact against the oracle on the upcast values; x's
+    gradient comes back in x's dtype (autograd of the cast), equal to the
+    oracle's fp32 gradient rounded to that dtype.  Running under
+    torch.autocast changes nothing."""
+    case = synthetic.make_case('det')
+    module = pkg.BevPoolTransform(case.xbound, case.ybound, case.zbound).to(cuda)
+    xh = case.x.to(dtype)
+    gh = case.geom.to(dtype)
+    x = xh.to(cuda).requires_grad_(True)
+    with torch.autocast('cuda', dtype=dtype, enabled=autocast):
+        out = module.bev_pool(gh.to(cuda), x)
+    assert out.dtype == torch.float32
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(31))
+    out.backward(g.to(cuda))
+    torch.cuda.synchronize()
+    assert x.grad.dtype == dtype
+    dx, bx, nx = grid_of(case)
+    xr = xh.float().requires_grad_(True)
+    out_ref = ref.lss_bev_pool(gh.float(), xr, dx, bx, nx)
+    out_ref.backward(g)
+    assert_bit_equal(out, out_ref, f'{dtype} x: fp32 forward')
+    assert_bit_equal(x.grad, xr.grad.to(dtype), f'{dtype} x: gradient in x dtype')

@@ -224,11 +224,28 @@ def test_out_of_range_coords_raise(pkg, cuda):
     feats, coords = rand_case(100, 3, 1, 2, 3, 4, seed=1)
     # x == H at z == D-1: rank ((0*2 + 1)*3 + 3)*4 + 0 = 24 == B*D*H*W
     coords[17] = torch.tensor([3, 0, 1, 0], dtype=torch.int32)
+    # default: no host synchronisation in the call; the point is excluded and
+    # the error is raised once the device has passed the call
+    out = pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
+    keep = torch.arange(100) != 17
+    assert_bit_equal(out, ref.bev_pool(feats[keep], coords[keep], 1, 2, 3, 4), 'bad point excluded')
     with pytest.raises(RuntimeError, match='index 24 is out of bounds'):
-        pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
+        pkg.check_errors()
+    pkg.check_errors()  # reported once
+    # ... or by the next call of the library once the device has finished
+    pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match='index 24 is out of bounds'):
+        pkg.bev_pool(feats[keep].to(cuda), coords[keep].to(cuda), 1, 2, 3, 4)
+    # check_bounds='sync' raises in the call itself
+    with pytest.raises(RuntimeError, match='index 24 is out of bounds'):
+        pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4, check_bounds='sync')
     coords[17] = torch.tensor([0, 0, 0, -1], dtype=torch.int32)  # negative batch
     with pytest.raises(RuntimeError, match='out of bounds'):
-        pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4)
+        pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4, check_bounds='sync')
+    # check_bounds=False: excluded, never reported
+    pkg.bev_pool(feats.to(cuda), coords.to(cuda), 1, 2, 3, 4, check_bounds=False)
+    pkg.check_errors()
     # a rank inside [0, B*D*H*W) is accepted even if one coordinate is out of
     # range: the reference flattens first (x = -1, y = 5 -> (-1)*4 + 5 = 1)
     coords[17] = torch.tensor([-1, 5, 0, 0], dtype=torch.int32)
@@ -249,3 +266,37 @@ def test_zero_channels(pkg, cuda):
     out = pkg.bev_pool(torch.zeros(5, 0, device=cuda), torch.zeros(5, 4, dtype=torch.int32,
                                                                     device=cuda), 1, 1, 1, 1)
     assert out.shape == (1, 0, 1, 1, 1)
+
+
+def test_op_entry_zero_dropped_flag(pkg, cuda):
+    """bevpool_op_forward / bevpool_op_backward through the C ABI (the
+    one-call op level): the forward equals the oracle; the backward with
+    zero_dropped = 1 writes zero rows for invalid coords, with
+    zero_dropped = 0 leaves them as the caller had them."""
+    from bevfusion_triton_amd import _lib as L
+    from bevfusion_triton_amd import _pipeline as P
+
+    sizes = (2, 1, 12, 13)
+    feats, coords = rand_case(5000, 20, *sizes, seed=21)
+    # flattened ranks 312 (= B*D*H*W), 312 and -1: outside [0, 312)
+    coords[[3, 77, 4999]] = torch.tensor([[12, 0, 0, 1], [0, 0, 0, 2], [0, -1, 0, 0]],
+                                         dtype=torch.int32)
+    keep = torch.ones(5000, dtype=torch.bool)
+    keep[[3, 77, 4999]] = False
+    f, c = feats.to(cuda), coords.to(cuda)
+    ws = P.op_workspace(5000, 2 * 12 * 13, 20, cuda)
+    out = torch.empty((2, 20, 1, 12, 13), device=cuda)
+    P.op_forward(f, c, *sizes, out, ws)
+    assert_bit_equal(out, ref.bev_pool(feats[keep], coords[keep], *sizes), 'op entry forward')
+    meta = P.op_meta(ws).cpu()
+    assert int(meta[L.META_N_BAD]) == 3 and int(meta[L.META_FIRST_BAD]) == 3
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(22)).to(cuda)
+    exp = torch.zeros(5000, 20)
+    exp[keep] = ref.backward_gather(g.cpu(), coords[keep], *sizes)
+    xg = torch.full((5000, 20), 7.0, device=cuda)
+    P.op_backward(g, 20, 5000, *sizes, xg, ws, zero_dropped=True)
+    assert_bit_equal(xg, exp, 'zero_dropped = 1')
+    xg = torch.full((5000, 20), 7.0, device=cuda)
+    P.op_backward(g, 20, 5000, *sizes, xg, ws, zero_dropped=False)
+    exp[~keep] = 7.0
+    assert_bit_equal(xg, exp, 'zero_dropped = 0')

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(pkg):
     lib = pkg.library()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.bevpool_abi_version() == 1
+    assert lib.bevpool_abi_version() == 2
     assert lib.bevpool_last_error() == b''
 
 
@@ -198,3 +198,32 @@ def test_status_codes_new_entry_points_without_gpu(pkg):
                                       f3(0, 0, 0), f3(1, 1, 1), i3(4, 4, 1), rank.ctypes.data,
                                       meta.ctypes.data, ws.ctypes.data, ws.size, None)
     assert st == -1 and b'camera matrices' in lib.bevpool_last_error()
+
+
+def test_legacy_ext_module_surface(pkg):
+    """The reference's tests/test_ops/test_bev_pool.py:50-54 against the
+    drop-in legacy module: an ``ext_module`` with both extension functions."""
+    legacy_ref_mod = pkg.legacy
+    assert hasattr(legacy_ref_mod, 'ext_module')
+    assert hasattr(legacy_ref_mod.ext_module, 'bev_pool_forward')
+    assert hasattr(legacy_ref_mod.ext_module, 'bev_pool_backward')
+
+
+def test_op_and_legacy_status_codes(pkg):
+    lib = pkg.library()
+    ws = np.zeros(1 << 12, np.uint8)
+    need = lib.bevpool_op_workspace_bytes(1000, 100, 8)
+    assert need > 1000 * 12 + 100 * 8 * 4 and need % 256 == 0
+    st = lib.bevpool_op_forward(None, 0, 8, 8, None, 4, 4, 1000, 1, 1, 10, 10, None,
+                                ws.ctypes.data, ws.size, None)
+    assert st == -3 and b'op workspace' in lib.bevpool_last_error()
+    st = lib.bevpool_op_forward(None, 0, 8, 8, None, 4, 4, 10, 1, 0, 10, 10, None,
+                                ws.ctypes.data, ws.size, None)
+    assert st == -1
+    st = lib.bevpool_legacy_forward(None, 10, 0, None, None, None, 0, None, 1, 1, 1, 1,
+                                    ws.ctypes.data, None, None)
+    assert st == -1 and b'C must be positive' in lib.bevpool_last_error()
+    st = lib.bevpool_runs(None, 2, 10, None, None, ws.ctypes.data, ws.ctypes.data, ws.size, None)
+    assert st == -1 and b'rank_bytes' in lib.bevpool_last_error()
+    st = lib.bevpool_runs(None, 8, 1 << 20, None, None, ws.ctypes.data, ws.ctypes.data, 16, None)
+    assert st == -3
