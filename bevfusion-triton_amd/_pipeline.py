@@ -377,47 +377,60 @@ def backward_depth(idx: PoolIndex, grad, C: int, stride_b: int, stride_c: int, s
 # the way an asynchronous device error does.
 
 class _Pending:
-    __slots__ = ('event', 'host', 'report')
+    __slots__ = ('event', 'ready', 'host', 'report', 'slot')
 
-    def __init__(self, event, host, report):
-        self.event, self.host, self.report = event, host, report
+    def __init__(self, event, ready, host, report, slot):
+        self.event, self.ready, self.host, self.report, self.slot = event, ready, host, report, slot
 
 
 _pending = []
-_side_streams = {}
 
 
-def _side_stream(device):
-    """A stream of the library's own per device (default priority) for the
-    counter read-backs, so they never queue behind or ahead of the caller's
-    work on the caller's stream."""
-    s = _side_streams.get(device)
-    if s is None:
-        s = _side_streams[device] = torch.cuda.Stream(device=device)
-    return s
+class _ReadBack:
+    """Per-device state of the counter read-backs: a stream of the library's
+    own (default priority), so they never queue on the caller's stream; one
+    pinned host buffer of ``_SLOTS`` meta records; reusable events."""
+
+    _SLOTS = 64
+
+    def __init__(self, device):
+        self.stream = torch.cuda.Stream(device=device)
+        self.host = torch.empty((self._SLOTS, L.META_LEN), dtype=torch.int32, pin_memory=True)
+        self.free = list(range(self._SLOTS))
+        self.events = []
+
+    def event(self):
+        return self.events.pop() if self.events else torch.cuda.Event()
+
+
+_readback = {}
 
 
 def defer_check(meta, report) -> None:
     """Queue a check of the device counters ``meta`` (int32, written by work
     already queued on the current stream).  An event marks that point on
     the caller's stream; the library's side stream waits for it and copies
-    the counters to pinned host memory, so the caller's stream carries only
+    the counters into a pinned host slot, so the caller's stream carries only
     the event.  ``report(host_meta)`` raises if they show an error.  Skipped
     while the stream is being captured into a graph."""
     if torch.cuda.is_current_stream_capturing():
         return
     device = meta.device
-    host = torch.empty(L.META_LEN, dtype=torch.int32, pin_memory=True)
-    ready = torch.cuda.Event()
+    rb = _readback.get(device)
+    if rb is None:
+        rb = _readback[device] = _ReadBack(device)
+    if not rb.free:
+        poll_errors(block=True)  # every slot awaits its copy: drain them
+    slot = rb.free.pop()
+    ready = rb.event()
     ready.record()
-    side = _side_stream(device)
-    side.wait_event(ready)
-    with torch.cuda.stream(side):
-        host.copy_(meta[:L.META_LEN], non_blocking=True)
-        done = torch.cuda.Event()
+    rb.stream.wait_event(ready)
+    with torch.cuda.stream(rb.stream):
+        rb.host[slot].copy_(meta[:L.META_LEN], non_blocking=True)
+        done = rb.event()
         done.record()
-    meta.record_stream(side)  # the allocator keeps meta until the copy has run
-    _pending.append(_Pending(done, host, report))
+    meta.record_stream(rb.stream)  # the allocator keeps meta until the copy has run
+    _pending.append(_Pending(done, ready, rb, report, slot))
 
 
 def poll_errors(block: bool = False) -> None:
@@ -430,7 +443,11 @@ def poll_errors(block: bool = False) -> None:
         elif not head.event.query():
             return
         _pending.pop(0)
-        head.report(head.host.numpy())
+        rb = head.host
+        meta = rb.host[head.slot].numpy().copy()
+        rb.free.append(head.slot)
+        rb.events += [head.event, head.ready]  # both have completed: reusable
+        head.report(meta)
 
 
 def coords_report(coords, B, D, H, W):
