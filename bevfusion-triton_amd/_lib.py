@@ -78,6 +78,10 @@ _SIGNATURES = {
          _vp],
         ctypes.c_int,
     ),
+    'bevpool_op_forward_noalloc': (
+        [_vp, _i32, _i64, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp],
+        ctypes.c_int,
+    ),
     'bevpool_op_backward': (
         [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp,
          _sz, _vp],

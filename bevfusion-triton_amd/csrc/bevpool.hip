@@ -173,6 +173,9 @@ struct TimingTotal {
 };
 std::mutex g_timing_mu;
 bool g_timing_enabled = false;
+// Set while an allocation-free entry point runs on this thread: its launches
+// are never bracketed by timing events (creating one may allocate).
+thread_local bool g_no_alloc_call = false;
 std::vector<TimingRecord> g_timing_pending;
 std::vector<hipEvent_t> g_event_pool;
 std::vector<std::pair<std::string, TimingTotal>> g_timing_totals;
@@ -194,6 +197,7 @@ struct LaunchTimer {
   hipStream_t stream;
   hipEvent_t start = nullptr, stop = nullptr;
   LaunchTimer(const char *n, hipStream_t s) : name(n), stream(s) {
+    if (g_no_alloc_call) return;
     std::lock_guard<std::mutex> lk(g_timing_mu);
     if (!g_timing_enabled) return;
     start = take_event();
@@ -2805,6 +2809,47 @@ OpLayout op_layout(int64_t n, int64_t cells, int32_t C) {
   return L;
 }
 
+// Scratch of the allocation-free op-level forward: the whole op workspace
+// (op_layout) of one call lives in this array, one copy per GPU, held until
+// the process ends.  Host code never passes `scratch` itself to a kernel or
+// a copy (in host code the name is a host-side stand-in, not a device
+// address): it uses the device address hipGetSymbolAddress returns for the
+// current device, cached per device by noalloc_scratch().
+constexpr size_t kNoAllocScratchBytes = BEVPOOL_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (resolved once per
+// device, with that device current), or nullptr with the error recorded.
+void *noalloc_scratch() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(BEVPOOL_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(BEVPOOL_EINVAL, "device %d beyond the %d devices the scratch table holds", dev,
+         kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(BEVPOOL_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+           hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -3557,6 +3602,33 @@ int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_strid
   return bevpool_forward(feats, dtype, feats_row_stride, C, n_points, keys, cstart, cend, meta, B,
                          D, hw, int64_t(C) * D * hw, int64_t(D) * hw, hw, out, ws + L.scratch,
                          size_t(cells) * size_t(C) * sizeof(float), stream);
+}
+
+int bevpool_op_forward_noalloc(const void *feats, int32_t dtype, int64_t feats_row_stride,
+                               int32_t C, const void *coords, int32_t coord_bytes,
+                               int64_t coords_row_stride, int64_t n_points, int32_t B, int32_t D,
+                               int32_t H, int32_t W, void *out, void *stream) {
+  g_last_error.clear();
+  if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range", (long long)n_points);
+  const int64_t cells = int64_t(B) * D * H * W;
+  if (cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "B*D*H*W exceeds 2^31-1");
+  const size_t need = op_layout(n_points, cells, C).total;
+  if (need > kNoAllocScratchBytes)
+    return fail(BEVPOOL_ESPACE,
+                "the allocation-free forward needs %zu bytes of scratch for n_points=%lld, "
+                "B*D*H*W=%lld, C=%d; its static scratch holds %zu (use bevpool_op_forward)",
+                need, (long long)n_points, (long long)cells, C, kNoAllocScratchBytes);
+  void *ws = noalloc_scratch();
+  if (!ws) return BEVPOOL_EHIP;
+  g_no_alloc_call = true;
+  const int st = bevpool_op_forward(feats, dtype, feats_row_stride, C, coords, coord_bytes,
+                                    coords_row_stride, n_points, B, D, H, W, out, ws,
+                                    kNoAllocScratchBytes, stream);
+  g_no_alloc_call = false;
+  return st;
 }
 
 int bevpool_op_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,

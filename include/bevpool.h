@@ -359,6 +359,27 @@ int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_strid
                        void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * bevpool_op_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  The workspace lives in a static device array of
+ * BEVPOOL_NOALLOC_MAX_BYTES bytes inside the library, one per GPU, held until
+ * the process ends; a call whose workspace (bevpool_op_workspace_bytes)
+ * exceeds it returns BEVPOOL_ESPACE.  The call allocates nothing (no
+ * hipMalloc, no events even with timing enabled).  Every call on one GPU
+ * uses that GPU's array, which keeps the last call's contents: calls that
+ * overlap on one GPU (concurrent streams or threads) race, and the index
+ * left behind is not kept for a backward.  Points with invalid coords are
+ * excluded, as in bevpool_op_forward; the count is not reported.
+ */
+#define BEVPOOL_NOALLOC_MAX_BYTES ((size_t)96 << 20)
+
+int bevpool_op_forward_noalloc(const void *feats, int32_t dtype, int64_t feats_row_stride,
+                               int32_t C, const void *coords, int32_t coord_bytes,
+                               int64_t coords_row_stride, int64_t n_points, int32_t B, int32_t D,
+                               int32_t H, int32_t W, void *out, void *stream);
+
+/*
  * Backward of bevpool_op_forward (bev_pool_triton.py:189-216): x_grad[p, :]
  * = grad at p's cell, on the index the last bevpool_op_forward left in the
  * workspace.  grad element (b, c, z, xy) at b*grad_stride_b + c*grad_stride_c
