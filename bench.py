@@ -204,11 +204,13 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--profile-steps', type=int, default=10,
                     help='steps run with per-kernel HIP-event timing')
-    ap.add_argument('--mode', default='bench', choices=['bench', 'kernels', 'configs'],
+    ap.add_argument('--mode', default='bench', choices=['bench', 'kernels', 'configs', 'ceiling'],
                     help="'kernels': run --steps plain fwd+bwd steps and a 512 MiB device copy "
                          "(the traffic calibrator for rocprofv3 --pmc passes), print nothing; "
                          "'configs': fwd/bwd time of every benchmark configuration, one JSON "
-                         'line each')
+                         "line each; 'ceiling': the accumulation kernel on the real index and on "
+                         'synthetic indexes whose rows are read in memory order or in random '
+                         'cell order, next to torch sum/fill/copy rates')
     ap.add_argument('--fold-pmc', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='fold the counter_collection.csv files of a FETCH_SIZE and a WRITE_SIZE '
                          'pass of --mode kernels into profiles/traffic_<config>.json (no GPU)')
@@ -229,6 +231,9 @@ def main():
     if args.mode == 'configs':
         for name in CONFIG_TABLE:
             print(json.dumps(config_figure(pkg, _lib, name, dev)), flush=True)
+        return
+    if args.mode == 'ceiling':
+        print(json.dumps(access_ceiling(pkg, _lib, args.config, dev)), flush=True)
         return
     log(f'[bench] building inputs for {args.config}')
     spec, geom_cpu, x_dev = make_inputs(pkg, args.config, dev)
@@ -541,6 +546,106 @@ def config_figure(pkg, lib, name, dev):
         'accum_rows_GBps': round(acc_b / (acc_us * 1e-6) / 1e9, 1) if acc_us else None,
         'kernels_us_per_step': {k: round(v, 1) for k, v in sorted(kt.items())},
     }
+
+
+def access_ceiling(pkg, lib, name, dev):
+    """How much of the forward accumulation's time is its row access order.
+    ``bevpool_forward`` (accumulation + transpose, library launch timers) runs
+    on the same features with three indexes of the same size:
+      * real: the sorted keys of the rig (each cell's points in point order);
+      * memory_order: cells of 39 consecutive sorted positions whose points are
+        consecutive rows, so the rows stream through memory in address order;
+      * random_cells: the real cells and chains, cells visited in a random
+        order (identical sums, checked).
+    Next to them, for scale: torch's own reduction over the whole feature
+    tensor (a library read, not a ceiling), a fill and a copy of the same
+    size (the copy counts its read and its write), all HIP-event timed
+    (median of 10)."""
+    from bevfusion_triton_amd import _pipeline as P
+
+    spec, geom_cpu, x = make_inputs(pkg, name, dev)
+    module = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(dev)
+    off, d, nx = module.grid()
+    idx = P.index_from_geom(geom_cpu.to(dev).reshape(-1, 3), spec.batch, off, d, nx)
+    n_kept = int(P.read_meta(idx)[0])
+    cells, C = idx.n_cells, spec.channels
+    X, Y, Z = (int(v) for v in nx)
+    x2 = x.reshape(-1, C)
+    out = torch.empty((spec.batch, C * Z, X, Y), device=dev)
+    scratch = torch.empty(cells * C * 4, dtype=torch.uint8, device=dev)
+    L = lib.library()
+
+    def run(keys, cs, ce, reps=20):
+        s = lib.stream_handle(dev)
+
+        def once():
+            lib.check(L.bevpool_forward(
+                lib.ptr(x2), 0, C, C, x2.shape[0], lib.ptr(keys), lib.ptr(cs), lib.ptr(ce),
+                lib.ptr(idx.meta), spec.batch, Z, X * Y, Z * C * X * Y, X * Y, C * X * Y,
+                lib.ptr(out), lib.ptr(scratch), scratch.numel(), s), 'bevpool_forward')
+        for _ in range(3):
+            once()
+        lib.timing_reset()
+        lib.timing_enable(True)
+        for _ in range(reps):
+            once()
+        torch.cuda.synchronize()
+        lib.timing_enable(False)
+        return {k: round(ms * 1e3 / n, 1) for k, (ms, n) in lib.timing_read().items()}
+
+    res = {'workload': WORKLOAD[name], 'n_kept': n_kept,
+           'row_bytes_read': n_kept * C * 4}
+    res['real'] = run(idx.keys, idx.cell_start, idx.cell_end)
+    ref_out = out.clone()
+    # memory order: cells of 39 consecutive positions, point index = position
+    pos = torch.arange(n_kept, device=dev, dtype=torch.int64)
+    rank = pos // 39
+    ncell = int(rank[-1].item()) + 1 if n_kept else 0
+    keys = torch.cat([(rank << 32) | pos, idx.keys[n_kept:]])
+    cs = torch.zeros(cells, dtype=torch.int32, device=dev)
+    ce = torch.zeros_like(cs)
+    cs[:ncell] = (torch.arange(ncell, device=dev) * 39).int()
+    ce[:ncell] = torch.clamp((torch.arange(ncell, device=dev) + 1) * 39, max=n_kept).int()
+    res['memory_order'] = run(keys, cs, ce)
+    # random cell order: the real chains, cells visited in a random order
+    k_cpu = idx.keys[:n_kept].cpu()
+    cs0, ce0 = idx.cell_start.cpu().long(), idx.cell_end.cpu().long()
+    occ = torch.nonzero(ce0 > cs0).squeeze(1)
+    order = occ[torch.randperm(occ.numel(), generator=torch.Generator().manual_seed(0))]
+    lens = (ce0 - cs0)[order]
+    starts = torch.cumsum(lens, 0) - lens
+    pieces = [k_cpu[a:b] for a, b in zip(cs0[order].tolist(), ce0[order].tolist())]
+    cs2 = torch.zeros(cells, dtype=torch.int32)
+    ce2 = torch.zeros(cells, dtype=torch.int32)
+    cs2[order] = starts.int()
+    ce2[order] = (starts + lens).int()
+    keys2 = torch.cat([torch.cat(pieces), idx.keys[n_kept:].cpu()]).to(dev)
+    res['random_cells'] = run(keys2, cs2.to(dev), ce2.to(dev))
+    res['random_cells']['same_output'] = bool(torch.equal(out, ref_out))
+    for k in ('real', 'memory_order', 'random_cells'):
+        us = res[k].get('accum_rows')
+        if us:
+            res[k]['accum_GBps'] = round(res['row_bytes_read'] / (us * 1e-6) / 1e9, 1)
+
+    def timed(fn, nbytes, reps=10):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return round(nbytes / (statistics.median(ts) * 1e-3) / 1e9, 1)
+
+    nbytes = x.numel() * 4
+    other = torch.empty_like(x)
+    res['torch_sum_read_GBps'] = timed(lambda: x.sum(), nbytes)
+    res['fill_GBps'] = timed(lambda: other.fill_(1.0), nbytes)
+    res['copy_GBps'] = timed(lambda: other.copy_(x), 2 * nbytes)
+    return res
 
 
 def op_level(pkg, geom, x, module, dev):

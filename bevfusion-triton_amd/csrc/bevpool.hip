@@ -850,8 +850,8 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 // the second walk drains each batch's loads before its first key store:
 // vmcnt counts loads and stores together, so a wait for a load issued after
 // a store would also wait for the store.  Dynamic LDS:
-// kBucketWaves * 2^lbits ints (16 waves up to 512 digits, 8 at 1024: at most
-// 64 KB per block).
+// kBucketWaves * 2^lbits ints (16 waves, up to 512 digits: at most 32 KB per
+// block).  Groups of 1024 cells take the sliced form below instead.
 
 template <int kBucketWaves>
 __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
@@ -961,6 +961,251 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
         keys_out[pos] = key[j];
         if (below == 0) cnt[dg] = pos + __popcll(peers);
       }
+    }
+  }
+}
+
+// Sliced form of the second half of the sort (same result as
+// bucket_sort_kernel).  Each group of equal high digit, in point order after
+// the global pass, is cut into slices of kSliceKeys consecutive keys, so that
+// a large group (the cells near the cameras: up to ~65 K keys at 2 x 720 x
+// 720) is spread over several blocks instead of being walked by one:
+//   bucket_count_kernel   one block per slice: the slice's low-digit counts;
+//   bucket_scan_kernel    one block per group: each slice's first sorted
+//                         position per digit (in place of its counts) and
+//                         the group's dense cell ranges;
+//   bucket_place_kernel   one block per slice: each key to its position
+//                         (the ranking of bucket_sort_kernel within a slice).
+// Slices are numbered group by group; a block finds its slice from the group
+// sizes (exclusive scans over the <= 1024 groups), so no kernel waits on
+// another block.
+constexpr int kSliceKeys = 8192;
+// Groups of 2^kSlicedBits cells take the sliced form.  Smaller groups (at
+// most ~35 K keys measured) take bucket_sort_kernel, whose one launch is
+// faster there (MI355X: 21.6 against 41 us at 1 x 360 x 360, 51 against 74
+// at 4 x 360 x 360); at 2^10 cells per group the sliced form takes 109
+// against 148 us (2 x 720 x 720).
+constexpr int kSlicedBits = 10;
+constexpr int kSliceWaves = 8;  // 8 waves x 2^10 per-wave digit counts: 32 KB of LDS
+
+template <int kW>
+struct SliceShape {
+  static constexpr int kT = 64 * kW;
+  static constexpr int kBatch = kSliceKeys / kT;  // 64-key sub-batches per wave
+  static_assert(kBatch * kT == kSliceKeys && kBatch <= 16, "slice shape");
+};
+
+__host__ __device__ inline int slices_of(int keys) {
+  return (keys + kSliceKeys - 1) / kSliceKeys;
+}
+
+// This block's slice: group g, slice id (== blockIdx.x; slices are numbered
+// group by group), sorted positions [first, end).  False (for the whole
+// block) past the last slice.  (Dealing the slices to the XCDs in 8
+// contiguous ranges, so that a group's interleaved writes share one L2, was
+// measured slower on MI355X.)
+struct SliceLoc {
+  int g, id, first, end;
+};
+
+template <int kW>
+__device__ bool find_slice(const int32_t *__restrict__ totals, int n_groups, SliceLoc *loc) {
+  constexpr int kT = 64 * kW;
+  constexpr int kG = (kMaxRadix + kT - 1) / kT;  // groups per thread
+  __shared__ int s_scan[kW];
+  __shared__ int s_loc[4];
+  const int tid = threadIdx.x;
+  int gn[kG], tk = 0, ts = 0;
+#pragma unroll
+  for (int i = 0; i < kG; ++i) {
+    const int g = tid * kG + i;
+    gn[i] = g < n_groups ? totals[g] : 0;
+    tk += gn[i];
+    ts += slices_of(gn[i]);
+  }
+  if (tid == 0) s_loc[0] = -1;  // ordered before the writes below by the scans' barriers
+  int unused, n_slices;
+  int kb = block_exclusive_scan<kW>(tk, s_scan, &unused);
+  int sb = block_exclusive_scan<kW>(ts, s_scan, &n_slices);
+  const int b = int(blockIdx.x);
+  if (b >= n_slices) return false;  // block-uniform
+#pragma unroll
+  for (int i = 0; i < kG; ++i) {
+    const int ns = slices_of(gn[i]);
+    if (b >= sb && b < sb + ns) {
+      const int first = kb + (b - sb) * kSliceKeys;
+      s_loc[0] = tid * kG + i;
+      s_loc[1] = b;
+      s_loc[2] = first;
+      s_loc[3] = gn[i] - (b - sb) * kSliceKeys < kSliceKeys ? kb + gn[i] : first + kSliceKeys;
+    }
+    sb += ns;
+    kb += gn[i];
+  }
+  __syncthreads();
+  loc->g = s_loc[0];
+  loc->id = s_loc[1];
+  loc->first = s_loc[2];
+  loc->end = s_loc[3];
+  return true;
+}
+
+// The keys of this wave's part of the slice (kBatch sub-batches of 64; past
+// the slice end they read its first key).
+template <int kW>
+__device__ __forceinline__ void load_slice_keys(const uint64_t *__restrict__ keys_in,
+                                                const SliceLoc &L, int w, int lane,
+                                                uint64_t (&key)[SliceShape<kW>::kBatch]) {
+  constexpr int kB = SliceShape<kW>::kBatch;
+  const int wb = L.first + w * 64 * kB;
+#pragma unroll
+  for (int j = 0; j < kB; ++j) {
+    const int e = wb + 64 * j + lane;
+    key[j] = keys_in[e < L.end ? e : L.first];
+  }
+}
+
+template <int kW>
+__global__ __launch_bounds__(64 * kW) void bucket_count_kernel(
+    const uint64_t *__restrict__ keys_in, const int32_t *__restrict__ totals, int n_groups,
+    int lbits, int32_t *__restrict__ slice_cnt) {
+  constexpr int kT = SliceShape<kW>::kT, kB = SliceShape<kW>::kBatch;
+  extern __shared__ int s_cnt[];  // [R]
+  SliceLoc L;
+  if (!find_slice<kW>(totals, n_groups, &L)) return;
+  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
+  const int R = 1 << lbits;
+  const unsigned mask = unsigned(R - 1);
+  uint64_t key[kB];
+  load_slice_keys<kW>(keys_in, L, w, lane, key);
+  for (int d = tid; d < R; d += kT) s_cnt[d] = 0;
+  __syncthreads();
+  const int wb = L.first + w * 64 * kB;
+#pragma unroll
+  for (int j = 0; j < kB; ++j)
+    if (wb + 64 * j < L.end)  // wave-uniform
+      count_digit_runs(s_cnt, key_digit(key[j], 0, mask), wb + 64 * j + lane < L.end);
+  __syncthreads();
+  int32_t *out = slice_cnt + int64_t(L.id) * R;
+  for (int d = tid; d < R; d += kT) out[d] = s_cnt[d];
+}
+
+__global__ __launch_bounds__(kThreads) void bucket_scan_kernel(
+    const int32_t *__restrict__ totals, int n_groups, int64_t n_cells, int lbits,
+    int32_t *__restrict__ slice_cnt, int32_t *__restrict__ cstart, int32_t *__restrict__ cend) {
+  __shared__ int s_scan[kWaves];
+  const int g = int(blockIdx.x);
+  if (g >= n_groups) return;
+  const int tid = threadIdx.x;
+  const int R = 1 << lbits;
+  // group start and first slice: sums over the groups before g
+  int pk = 0, ps = 0;
+  for (int d = tid; d < g; d += kThreads) {
+    const int t = totals[d];
+    pk += t;
+    ps += slices_of(t);
+  }
+  int gs, sb;
+  block_exclusive_scan(pk, s_scan, &gs);
+  block_exclusive_scan(ps, s_scan, &sb);
+  const int ns = slices_of(totals[g]);
+  int32_t *sc = slice_cnt + int64_t(sb) * R;
+  // thread t owns digits 4t .. 4t+3 (R is a multiple of 4, >= 32): the
+  // group's totals per digit, then the digit starts
+  constexpr int kU = 8;  // slices whose counts are loaded together
+  const int d0 = 4 * tid;
+  const bool mine = d0 < R;
+  u32x4 tot = {0u, 0u, 0u, 0u};
+  if (mine) {
+    for (int k0 = 0; k0 < ns; k0 += kU) {
+      u32x4 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        v[u] = k0 + u < ns ? *reinterpret_cast<const u32x4 *>(sc + int64_t(k0 + u) * R + d0)
+                           : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int u = 0; u < kU; ++u) tot += v[u];
+    }
+  }
+  int unused;
+  int ex = gs + block_exclusive_scan(int(tot.x + tot.y + tot.z + tot.w), s_scan, &unused);
+  if (!mine) return;
+  // first sorted position of each of the four digits in slice 0
+  u32x4 run;
+  run.x = uint32_t(ex);
+  run.y = run.x + tot.x;
+  run.z = run.y + tot.y;
+  run.w = run.z + tot.z;
+  const int64_t cell0 = int64_t(g) * R + d0;
+  const uint32_t t4[4] = {tot.x, tot.y, tot.z, tot.w};
+  const uint32_t r4[4] = {run.x, run.y, run.z, run.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (cell0 + i < n_cells) {
+      cstart[cell0 + i] = t4[i] ? int(r4[i]) : 0;
+      cend[cell0 + i] = t4[i] ? int(r4[i] + t4[i]) : 0;
+    }
+  }
+  for (int k0 = 0; k0 < ns; k0 += kU) {
+    u32x4 v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      v[u] = k0 + u < ns ? *reinterpret_cast<const u32x4 *>(sc + int64_t(k0 + u) * R + d0)
+                         : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (k0 + u < ns) *reinterpret_cast<u32x4 *>(sc + int64_t(k0 + u) * R + d0) = run;
+      run += v[u];
+    }
+  }
+}
+
+template <int kW>
+__global__ __launch_bounds__(64 * kW) void bucket_place_kernel(
+    const uint64_t *__restrict__ keys_in, const int32_t *__restrict__ totals, int n_groups,
+    int lbits, const int32_t *__restrict__ slice_cnt, uint64_t *__restrict__ keys_out) {
+  constexpr int kT = SliceShape<kW>::kT, kB = SliceShape<kW>::kBatch;
+  extern __shared__ int s_cnt[];  // [kW][R]
+  SliceLoc L;
+  if (!find_slice<kW>(totals, n_groups, &L)) return;
+  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
+  const int R = 1 << lbits;
+  const unsigned mask = unsigned(R - 1);
+  uint64_t key[kB];
+  load_slice_keys<kW>(keys_in, L, w, lane, key);
+  for (int d = tid; d < kW * R; d += kT) s_cnt[d] = 0;
+  __syncthreads();
+  int *cnt = s_cnt + w * R;
+  const int wb = L.first + w * 64 * kB;
+#pragma unroll
+  for (int j = 0; j < kB; ++j)
+    if (wb + 64 * j < L.end)
+      count_digit_runs(cnt, key_digit(key[j], 0, mask), wb + 64 * j + lane < L.end);
+  __syncthreads();
+  // per-wave bases: the slice's first position of the digit + earlier waves
+  const int32_t *base = slice_cnt + int64_t(L.id) * R;
+  for (int d = tid; d < R; d += kT) {
+    int run = base[d];
+#pragma unroll
+    for (int ww = 0; ww < kW; ++ww) {
+      const int c = s_cnt[ww * R + d];
+      s_cnt[ww * R + d] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  const uint64_t below_mask = lanes_below();
+#pragma unroll
+  for (int j = 0; j < kB; ++j) {
+    if (wb + 64 * j >= L.end) break;
+    const bool valid = wb + 64 * j + lane < L.end;
+    const unsigned dg = key_digit(key[j], 0, mask);
+    const uint64_t peers = peer_mask(dg, valid);
+    if (valid) {
+      const int below = __popcll(peers & below_mask);
+      const int pos = cnt[dg] + below;
+      keys_out[pos] = key[j];
+      if (below == 0) cnt[dg] = pos + __popcll(peers);
     }
   }
 }
@@ -1566,17 +1811,20 @@ __device__ __forceinline__ bool load_tile_cells(int64_t cell0, int64_t n_cells,
 // (channel-first, dtype T); empty cells are written as 0.  The tile holds the
 // raw fp32 bits, and a staged 16-byte piece is never converted lane by lane
 // to float (hipcc 7.2 with packed fp32 ops disabled folded bit casts of lanes
-// y/z/w of such a vector into lane x).  With kVecRow every row piece of the
-// tile is loaded up front (kTileSlots per thread, clamped in-bounds
-// addresses, empty cells included) together with the occupancy loads, so a
-// block pays one memory latency before its stores.  Occupancy: cell_end != 0
-// (cell ranges are zeroed before the sort writes the occupied ones).
+// y/z/w of such a vector into lane x).  With kVecRow each wave first reads
+// the tile's 64 cell ends as a ballot mask, then loads every row piece of the
+// occupied cells up front (kTileSlots per thread, clamped in-bounds
+// addresses), so a block pays two memory latencies before its stores and
+// reads no row of an empty cell (measured on MI355X: 53 -> 43 us at B = 4,
+// 360 x 360, unchanged at B = 1).  Occupancy: cell_end != 0 (cell ranges are
+// zeroed before the sort writes the occupied ones).
 constexpr int kTileSlots = kCellTile * (kTileChannels / 4) / kThreads;  // 8
 // bev_to_rows on grids of at least this many cells reads the occupancy of a
 // thread's 4 cells before its gradient loads (one more memory latency per
 // block, no loads for 4 empty cells); smaller grids issue every load up
 // front.  Measured on MI355X: 3-10% faster from 518,400 cells (B = 4 at
-// 360 x 360) up, slower at 129,600.  The same for rows_to_bev was slower.
+// 360 x 360) up, slower at 129,600.  The same per-thread scheme for
+// rows_to_bev was slower (it uses the wave-wide mask above instead).
 constexpr int64_t kOccFirstCells = 200000;
 
 template <typename T, bool kVecRow, bool kVecBev>
@@ -1599,6 +1847,15 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
   }
   const uint32_t *accb = reinterpret_cast<const uint32_t *>(acc);
   const int pitch = CT + 1;
+  // occupancy of the tile's 64 cells as a mask in every wave (lane j loads
+  // cell j's end), so that only occupied cells' rows are loaded: one more
+  // dependent load, and no row bytes for empty cells (most cells of the
+  // sparser grids)
+  uint64_t occm = 0;
+  if (kVecRow) {
+    const int64_t cj = cell0 + lane_id();
+    occm = __ballot(cj < n_cells && cend[cj] != 0);
+  }
   if (!kVecRow) {
     if (tid < kCellTile) {
       occ[tid] = occ_mine;
@@ -1617,7 +1874,9 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
         const uint32_t i = tid + it * kThreads;
         uint32_t t = i / q, k = i - t * q;
         if (i >= n_items || cell0 + t >= n_cells) t = k = 0;
-        v[it] = *reinterpret_cast<const u32x4 *>(accb + (cell0 + t) * C + c0 + 4 * k);
+        v[it] = ((occm >> t) & 1)
+                    ? *reinterpret_cast<const u32x4 *>(accb + (cell0 + t) * C + c0 + 4 * k)
+                    : u32x4{0u, 0u, 0u, 0u};
       }
       if (c0 == 0 && tid < kCellTile) {
         occ[tid] = occ_mine;
@@ -2534,11 +2793,25 @@ DigitPlan plan_digits(int64_t n_cells) {
 }
 
 struct IndexLayout {
-  size_t keys_tmp, hist, totals, bcount, total;
+  size_t keys_tmp, hist, totals, bcount, slices, total;
   int64_t sort_blocks, cell_blocks;
 };
 
-IndexLayout index_layout(int64_t n_points) {
+// Slices of the sliced bucket sort (an upper bound: every group may end in a
+// partial slice) and the bytes of their low-digit counts.
+int64_t slice_bound(int64_t n_points, int64_t n_cells, int lbits) {
+  return ceil_div(n_cells, int64_t(1) << lbits) + ceil_div(n_points, int64_t(kSliceKeys));
+}
+
+size_t slice_count_bytes(int64_t n_points, int64_t n_cells) {
+  const DigitPlan plan = plan_digits(n_cells);
+  if (plan.local_bits < kSlicedBits) return 0;
+  return size_t(slice_bound(n_points, n_cells, plan.local_bits)) << plan.local_bits << 2;
+}
+
+// Index-stage workspace.  The slice counts at the end depend on n_cells; a
+// caller that only uses the other regions may pass n_cells = 1.
+IndexLayout index_layout(int64_t n_points, int64_t n_cells) {
   IndexLayout L;
   L.sort_blocks = ceil_div(n_points, kSortTile);
   L.cell_blocks = ceil_div(n_points, kThreads);
@@ -2551,6 +2824,8 @@ IndexLayout index_layout(int64_t n_points) {
   o = align256(o + size_t(kMaxRadix) * sizeof(int32_t));
   L.bcount = o;
   o = align256(o + size_t(L.cell_blocks) * sizeof(int32_t));
+  L.slices = o;
+  o = align256(o + slice_count_bytes(n_points, n_cells));
   L.total = o;
   return L;
 }
@@ -2568,7 +2843,7 @@ int check_index_args(int64_t n_points, int64_t n_cells, const void *rank, const 
     return fail(BEVPOOL_EINVAL, "B*D*H*W=%lld out of range [1, 2^31)", (long long)n_cells);
   if (!meta || !ws) return fail(BEVPOOL_EINVAL, "null meta or workspace");
   if (n_points > 0 && !rank) return fail(BEVPOOL_EINVAL, "null rank");
-  const size_t need = index_layout(n_points).total;
+  const size_t need = index_layout(n_points, n_cells).total;
   if (ws_bytes < need)
     return fail(BEVPOOL_ESPACE, "index workspace %zu bytes < required %zu", ws_bytes, need);
   return BEVPOOL_OK;
@@ -2802,7 +3077,7 @@ OpLayout op_layout(int64_t n, int64_t cells, int32_t C) {
   L.cend = o;
   o = align256(o + size_t(cells) * sizeof(int32_t));
   L.index_ws = o;
-  o = align256(o + index_layout(n).total);
+  o = align256(o + index_layout(n, cells).total);
   L.scratch = o;
   o = align256(o + size_t(cells) * size_t(C) * sizeof(float));
   L.total = o;
@@ -2862,9 +3137,8 @@ int bevpool_abi_version(void) { return BEVPOOL_ABI_VERSION; }
 const char *bevpool_last_error(void) { return g_last_error.c_str(); }
 
 size_t bevpool_index_workspace_bytes(int64_t n_points, int64_t n_cells) {
-  (void)n_cells;
   if (n_points < 0) return 0;
-  return index_layout(n_points).total;
+  return index_layout(n_points, n_cells < 1 ? 1 : n_cells).total;
 }
 
 int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_stride,
@@ -2884,7 +3158,7 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
     return fail(BEVPOOL_EINVAL, "bad geometry layout (row stride %lld, points/batch %lld)",
                 (long long)geom_row_stride, (long long)points_per_batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const IndexLayout L = index_layout(n_points);
+  const IndexLayout L = index_layout(n_points, n_cells);
   const DigitPlan plan = plan_digits(n_cells);
   {
     // also resets meta (block 0); an empty input still launches that block
@@ -2929,7 +3203,7 @@ int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_
   if (!frustum || !rots || !trans || !intrins || !post_rots || !post_trans)
     return fail(BEVPOOL_EINVAL, "null frustum/camera matrices");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const IndexLayout L = index_layout(n_points);
+  const IndexLayout L = index_layout(n_points, n_cells);
   const DigitPlan plan = plan_digits(n_cells);
   const CameraMats cm{rots, trans, intrins, post_rots, post_trans, extra_rots, extra_trans,
                       n_cams_per_batch};
@@ -2964,7 +3238,7 @@ int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_point
   }
   if ((st = check_launch("init_meta"))) return st;
   if (n_points == 0) return BEVPOOL_OK;
-  const IndexLayout L = index_layout(n_points);
+  const IndexLayout L = index_layout(n_points, n_cells);
   const DigitPlan plan = plan_digits(n_cells);
   LaunchTimer t("coord_ranks", s);
   if (coord_bytes == 4) {
@@ -2992,7 +3266,7 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
   if (!cell_start || !cell_end) return fail(BEVPOOL_EINVAL, "null cell_start/cell_end");
   if (n_points > 0 && !keys) return fail(BEVPOOL_EINVAL, "null keys");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const IndexLayout L = index_layout(n_points);
+  const IndexLayout L = index_layout(n_points, n_cells);
   const DigitPlan plan = plan_digits(n_cells);
   int32_t *hist = at<int32_t>(workspace, L.hist);
   int32_t *totals = at<int32_t>(workspace, L.totals);
@@ -3037,19 +3311,40 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
     }
     src = dst;
   }
+  if (bucketed && plan.local_bits >= kSlicedBits) {
+    // groups of 2^10 cells (up to ~65 K keys at 2 x 720 x 720), cut into
+    // slices -> sorted keys and the dense cell ranges
+    const int lb = plan.local_bits;
+    const int n_groups = int(ceil_div(n_cells, int64_t(1) << lb));
+    const int64_t n_slices = slice_bound(n_points, n_cells, lb);
+    if ((st = check_grid(n_slices, kThreads, "bucket slices"))) return st;
+    int32_t *scnt = at<int32_t>(workspace, L.slices);
+    const size_t R4 = size_t(4) << lb;
+    {
+      LaunchTimer t("bucket_count", s);
+      hipLaunchKernelGGL(bucket_count_kernel<kSliceWaves>, dim3(unsigned(n_slices)),
+                         dim3(64 * kSliceWaves), R4, s, src, totals, n_groups, lb, scnt);
+      if ((st = check_launch("bucket_count"))) return st;
+    }
+    {
+      LaunchTimer t("bucket_scan", s);
+      hipLaunchKernelGGL(bucket_scan_kernel, dim3(unsigned(n_groups)), dim3(kThreads), 0, s,
+                         totals, n_groups, n_cells, lb, scnt, cell_start, cell_end);
+      if ((st = check_launch("bucket_scan"))) return st;
+    }
+    LaunchTimer t("bucket_place", s);
+    hipLaunchKernelGGL(bucket_place_kernel<kSliceWaves>, dim3(unsigned(n_slices)),
+                       dim3(64 * kSliceWaves), kSliceWaves * R4, s, src, totals, n_groups, lb,
+                       scnt, keys);
+    return check_launch("bucket_place");
+  }
   if (bucketed) {
-    // groups of equal high digit -> sorted keys and the dense cell ranges
+    // groups of at most 2^9 cells -> sorted keys and the dense cell ranges
     LaunchTimer t("bucket_sort", s);
     const int64_t n_buckets = ceil_div(n_cells, int64_t(1) << plan.local_bits);
-    if (plan.local_bits <= 9) {
-      hipLaunchKernelGGL(bucket_sort_kernel<16>, dim3(unsigned(n_buckets)), dim3(16 * 64),
-                         size_t(16) << plan.local_bits << 2, s, src, totals, int(n_buckets),
-                         n_cells, keys, cell_start, cell_end, plan.local_bits);
-    } else {
-      hipLaunchKernelGGL(bucket_sort_kernel<8>, dim3(unsigned(n_buckets)), dim3(8 * 64),
-                         size_t(8) << plan.local_bits << 2, s, src, totals, int(n_buckets),
-                         n_cells, keys, cell_start, cell_end, plan.local_bits);
-    }
+    hipLaunchKernelGGL(bucket_sort_kernel<16>, dim3(unsigned(n_buckets)), dim3(16 * 64),
+                       size_t(16) << plan.local_bits << 2, s, src, totals, int(n_buckets),
+                       n_cells, keys, cell_start, cell_end, plan.local_bits);
     return check_launch("bucket_sort");
   }
   {
@@ -3072,7 +3367,7 @@ int bevpool_intervals(const uint64_t *keys, int64_t n_points, const int32_t *cel
   if (n_points < 0 || n_points > int64_t(INT32_MAX))
     return fail(BEVPOOL_EINVAL, "n_points out of range");
   if (!meta) return fail(BEVPOOL_EINVAL, "meta is null");
-  const IndexLayout L = index_layout(n_points);
+  const IndexLayout L = index_layout(n_points, 1);
   if (workspace_bytes < L.total) return fail(BEVPOOL_ESPACE, "index workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
   int32_t *bcount = at<int32_t>(workspace, L.bcount);
@@ -3592,7 +3887,7 @@ int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_strid
   int32_t *cstart = reinterpret_cast<int32_t *>(ws + L.cstart);
   int32_t *cend = reinterpret_cast<int32_t *>(ws + L.cend);
   void *iws = ws + L.index_ws;
-  const size_t iws_bytes = index_layout(n_points).total;
+  const size_t iws_bytes = index_layout(n_points, cells).total;
   int st = bevpool_coord_ranks(coords, coord_bytes, n_points, coords_row_stride, B, D, H, W,
                                rank, meta, iws, iws_bytes, stream);
   if (st) return st;

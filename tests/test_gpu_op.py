@@ -148,21 +148,38 @@ def test_shapes_and_edges(pkg, cuda, N, sizes, C):
     ('11-bit ranks, 2-cell groups', (1, 1, 5, 205)),
     ('20-bit ranks, 1024-cell groups', (1, 1, 1024, 1024)),
     ('17-bit ranks, one group holding most points', (1, 1, 360, 360)),
+    ('20-bit ranks, one group holding most points', (1, 1, 1024, 1024)),
+    ('20-bit ranks, groups at slice boundaries', (1, 1, 1024, 1024)),
 ])
 def test_bucket_sort_edges(pkg, cuda, name, sizes):
-    """Ranks of 11..20 bits: one global pass by the high 10 bits, then one
-    block per group sorts the low bits and writes the group's cell ranges.
-    Cases: the smallest groups, the largest rank space, and one group far
-    larger than the rest (90% of the points in 3 cells, sizes not multiples
-    of 64), with empty groups around it."""
+    """Ranks of 11..20 bits: one global pass by the high 10 bits, then the
+    low bits are sorted per group (one block per group of up to 512 cells;
+    groups of 1024 cells are cut into slices of 8192 keys) and the group's
+    cell ranges written.  Cases: the smallest groups, the largest rank space,
+    one group far larger than the rest (90% of the points in 3 cells, sizes
+    not multiples of 64) with empty groups around it, and groups of exactly
+    1, 2 and 4 slices and one key more."""
     N = 120000
     feats, coords = rand_case(N, 8, *sizes, seed=11)
     if 'one group' in name:
         g = torch.Generator().manual_seed(12)
         hot = torch.rand(N, generator=g) < 0.9
         cell = torch.randint(0, 3, (N,), generator=g)
-        coords[hot, 0] = 200  # x: cells 200*360 + 100..102 share one group
+        coords[hot, 0] = 200  # x: cells 200*W + 100..102 share one group
         coords[hot, 1] = 100 + cell[hot].to(coords.dtype)
+    if 'slice boundaries' in name:
+        # with W = 1024 the group of a point is its x: groups 5, 9, 11, 13,
+        # 17, 19 get 8192, 8193, 16384, 16385, 32768, 32769 points, spread
+        # over the point order; the other points fall in other groups
+        g = torch.Generator().manual_seed(13)
+        xs = torch.randint(0, 1024, (N,), generator=g)
+        xs[(xs == 5) | (xs == 9) | (xs == 11) | (xs == 13) | (xs == 17) | (xs == 19)] = 0
+        order = torch.randperm(N, generator=g)
+        at = 0
+        for x, n in ((5, 8192), (9, 8193), (11, 16384), (13, 16385), (17, 32768), (19, 32769)):
+            xs[order[at:at + n]] = x
+            at += n
+        coords[:, 0] = xs.to(coords.dtype)
     B, D, H, W = sizes
     exp = pkg.BevPoolIndexExport(coords.to(cuda), *sizes)
     ranks = ref.flatten_ranks(coords, *sizes)
