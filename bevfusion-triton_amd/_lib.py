@@ -17,11 +17,12 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime first; see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / 'libbevpool_amd.so'
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, F16, BF16 = 0, 1, 2
 META_N_KEPT, META_N_INTERVALS, META_N_BAD, META_FIRST_BAD = 0, 1, 2, 3
 META_LEN = 8
+REPORT_LEN = META_LEN + 1  # the counters, then a done flag
 
 DTYPE_CODES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -60,6 +61,7 @@ _SIGNATURES = {
     ),
     'bevpool_sort': ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
     'bevpool_intervals': ([_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
+    'bevpool_meta_report': ([_vp, _vp, _vp], ctypes.c_int),
     'bevpool_forward_scratch_bytes': ([_i64, _i32], _sz),
     'bevpool_forward': (
         [_vp, _i32, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _i64,
@@ -75,7 +77,7 @@ _SIGNATURES = {
     'bevpool_op_workspace_bytes': ([_i64, _i64, _i32], _sz),
     'bevpool_op_forward': (
         [_vp, _i32, _i64, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _sz,
-         _vp],
+         _vp, _vp],
         ctypes.c_int,
     ),
     'bevpool_op_forward_noalloc': (

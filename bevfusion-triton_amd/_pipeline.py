@@ -370,84 +370,106 @@ def backward_depth(idx: PoolIndex, grad, C: int, stride_b: int, stride_c: int, s
 #
 # The device counts invalid inputs (coords outside the grid, intervals outside
 # the arrays) in a meta array.  Reading it at once would synchronise the host
-# with the device on every call; instead the counters are copied to pinned
-# host memory on the call's stream, behind an event, and inspected once that
-# event has completed -- at the next call of the library's autograd
-# functions, or at check_errors().  An error therefore surfaces one call late,
-# the way an asynchronous device error does.
+# with the device on every call; instead a kernel of the call (the op-level
+# forward's last kernel, or bevpool_meta_report's single block) writes the
+# counters into a slot of pinned host memory and then sets the slot's done
+# flag, which the host polls -- at the next call of the library's autograd
+# functions, or at check_errors().  No event, copy or second stream is
+# involved.  An error therefore surfaces one call late, the way an
+# asynchronous device error does.
 
 class _Pending:
-    __slots__ = ('event', 'ready', 'host', 'report', 'slot')
+    __slots__ = ('host', 'report', 'slot')
 
-    def __init__(self, event, ready, host, report, slot):
-        self.event, self.ready, self.host, self.report, self.slot = event, ready, host, report, slot
+    def __init__(self, host, report, slot):
+        self.host, self.report, self.slot = host, report, slot
 
 
 _pending = []
 
 
 class _ReadBack:
-    """Per-device state of the counter read-backs: a stream of the library's
-    own (default priority), so they never queue on the caller's stream; one
-    pinned host buffer of ``_SLOTS`` meta records; reusable events."""
+    """Per-device pinned host buffer of ``_SLOTS`` report slots (the
+    counters, then the done flag; 64 bytes apart)."""
 
     _SLOTS = 64
+    _STRIDE = 16  # int32 per slot (>= REPORT_LEN)
 
     def __init__(self, device):
-        self.stream = torch.cuda.Stream(device=device)
-        self.host = torch.empty((self._SLOTS, L.META_LEN), dtype=torch.int32, pin_memory=True)
+        self.device = device
+        self.host = torch.zeros((self._SLOTS, self._STRIDE), dtype=torch.int32, pin_memory=True)
+        self.view = self.host.numpy()  # the same pinned memory, read without torch dispatch
+        self.base = self.host.data_ptr()
         self.free = list(range(self._SLOTS))
-        self.events = []
-
-    def event(self):
-        return self.events.pop() if self.events else torch.cuda.Event()
 
 
 _readback = {}
 
 
-def defer_check(meta, report) -> None:
-    """Queue a check of the device counters ``meta`` (int32, written by work
-    already queued on the current stream).  An event marks that point on
-    the caller's stream; the library's side stream waits for it and copies
-    the counters into a pinned host slot, so the caller's stream carries only
-    the event.  ``report(host_meta)`` raises if they show an error.  Skipped
-    while the stream is being captured into a graph."""
-    if torch.cuda.is_current_stream_capturing():
-        return
-    device = meta.device
+def report_slot(device):
+    """A free pinned slot for a deferred report on ``device``, its done flag
+    cleared: (state, slot, host address).  Drains the pending reports when
+    every slot is taken."""
     rb = _readback.get(device)
     if rb is None:
         rb = _readback[device] = _ReadBack(device)
     if not rb.free:
-        poll_errors(block=True)  # every slot awaits its copy: drain them
+        poll_errors(block=True)  # every slot awaits its kernel: drain them
     slot = rb.free.pop()
-    ready = rb.event()
-    ready.record()
-    rb.stream.wait_event(ready)
-    with torch.cuda.stream(rb.stream):
-        rb.host[slot].copy_(meta[:L.META_LEN], non_blocking=True)
-        done = rb.event()
-        done.record()
-    meta.record_stream(rb.stream)  # the allocator keeps meta until the copy has run
-    _pending.append(_Pending(done, ready, rb, report, slot))
+    rb.view[slot, L.META_LEN] = 0
+    return rb, slot, rb.base + slot * 4 * _ReadBack._STRIDE
+
+
+def defer_report(rb, slot, report) -> None:
+    """Queue ``report(host_meta)`` for slot ``slot``, which work already
+    queued on the current stream fills."""
+    _pending.append(_Pending(rb, report, slot))
+
+
+def defer_check(meta, report) -> None:
+    """Queue a check of the device counters ``meta`` (int32, written by work
+    already queued on the current stream): a single-block kernel on that
+    stream copies them into a pinned host slot and sets its done flag.
+    ``report(host_meta)`` raises if they show an error.  Skipped while the
+    stream is being captured into a graph."""
+    if torch.cuda.is_current_stream_capturing():
+        return
+    device = meta.device
+    rb, slot, addr = report_slot(device)
+    with torch.cuda.device(device):
+        st = L.library().bevpool_meta_report(L.ptr(meta), addr, L.stream_handle(device))
+        if st:
+            rb.free.append(slot)
+        L.check(st, 'bevpool_meta_report')
+    defer_report(rb, slot, report)
 
 
 def poll_errors(block: bool = False) -> None:
     """Raise the first deferred error whose device work has finished (all
-    queued ones when ``block``; that waits for them)."""
-    while _pending:
-        head = _pending[0]
-        if block:
-            head.event.synchronize()
-        elif not head.event.query():
-            return
-        _pending.pop(0)
-        rb = head.host
-        meta = rb.host[head.slot].numpy().copy()
-        rb.free.append(head.slot)
-        rb.events += [head.event, head.ready]  # both have completed: reusable
-        head.report(meta)
+    queued ones when ``block``; that waits for the devices)."""
+    if not _pending:
+        return
+    if block:
+        for dev in {p.host.device for p in _pending}:
+            torch.cuda.synchronize(dev)
+    done = []
+    keep = []
+    for p in _pending:
+        (done if p.host.view[p.slot, L.META_LEN] else keep).append(p)
+    if not done:
+        return
+    _pending[:] = keep
+    first = None
+    for p in done:
+        meta = p.host.view[p.slot, :L.META_LEN].copy()
+        p.host.free.append(p.slot)
+        try:
+            p.report(meta)
+        except RuntimeError as e:  # report every finished slot; raise the first error
+            if first is None:
+                first = e
+    if first is not None:
+        raise first
 
 
 def coords_report(coords, B, D, H, W):
@@ -481,17 +503,29 @@ def op_meta(ws):
     return ws[:4 * L.META_LEN].view(torch.int32)
 
 
-def op_forward(feats2d, coords, B, D, H, W, out, ws) -> None:
+def op_forward(feats2d, coords, B, D, H, W, out, ws, report=None) -> None:
+    """The one-call op-level forward.  ``report``: None, or a callable
+    ``report(host_meta)`` run on the meta counters once the device has passed
+    this call (the call's last kernel writes them and a done flag into a
+    pinned slot; no host synchronisation).  Not queued while the stream is
+    being captured."""
     n, C = feats2d.shape
-    with torch.cuda.device(feats2d.device):
-        L.check(
-            L.library().bevpool_op_forward(
-                L.ptr(feats2d), L.DTYPE_CODES[feats2d.dtype], feats2d.stride(0) if n else C, C,
-                L.ptr(coords), coords.element_size(), coords.stride(0) if n else 4, n, B, D, H,
-                W, L.ptr(out), L.ptr(ws), ws.numel(), L.stream_handle(feats2d.device),
-            ),
-            'bevpool_op_forward',
+    device = feats2d.device
+    slot = None
+    if report is not None and not torch.cuda.is_current_stream_capturing():
+        rb, slot, addr = report_slot(device)
+    with torch.cuda.device(device):
+        st = L.library().bevpool_op_forward(
+            L.ptr(feats2d), L.DTYPE_CODES[feats2d.dtype], feats2d.stride(0) if n else C, C,
+            L.ptr(coords), coords.element_size(), coords.stride(0) if n else 4, n, B, D, H,
+            W, L.ptr(out), L.ptr(ws), ws.numel(), addr if slot is not None else None,
+            L.stream_handle(device),
         )
+        if st and slot is not None:
+            rb.free.append(slot)
+        L.check(st, 'bevpool_op_forward')
+    if slot is not None:
+        defer_report(rb, slot, report)
 
 
 def op_backward(grad, C, n, B, D, H, W, x_grad, ws, zero_dropped=True) -> None:

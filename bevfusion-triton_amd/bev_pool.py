@@ -81,11 +81,14 @@ class BevPoolFunction(torch.autograd.Function):
         coords2d = coords if coords.stride(1) == 1 or N == 0 else coords.contiguous()
         ws = P.op_workspace(N, B * D * H * W, C, feats.device)
         out = torch.empty((B, C, D, H, W), dtype=feats.dtype, device=feats.device)
-        P.op_forward(feats2d, coords2d, B, D, H, W, out, ws)
         if check_bounds == 'sync':
+            P.op_forward(feats2d, coords2d, B, D, H, W, out, ws)
             P.coords_report(coords2d, B, D, H, W)(P.op_meta(ws).cpu().numpy())
         elif check_bounds:
-            P.defer_check(P.op_meta(ws), P.coords_report(coords2d, B, D, H, W))
+            P.op_forward(feats2d, coords2d, B, D, H, W, out, ws,
+                         report=P.coords_report(coords2d, B, D, H, W))
+        else:
+            P.op_forward(feats2d, coords2d, B, D, H, W, out, ws)
         ctx.ws = ws
         return out
 

@@ -672,6 +672,7 @@ __global__ void init_meta_kernel(int32_t *meta) {
     meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
 }
 
+
 // One block per digit: exclusive scan over the blocks of hist[d][*] in place,
 // totals[d] = row sum.  Optionally zeroes the dense cell ranges (grid-stride).
 __global__ __launch_bounds__(kThreads) void radix_scan_kernel(
@@ -1827,12 +1828,45 @@ constexpr int kTileSlots = kCellTile * (kTileChannels / 4) / kThreads;  // 8
 // rows_to_bev was slower (it uses the wave-wide mask above instead).
 constexpr int64_t kOccFirstCells = 200000;
 
+// Optional copy of the meta counters into memory the host reads (pinned host
+// memory through its device address), made by a kernel that runs anyway.
+// The counters go out as system-scope (written-through) stores; once they
+// are acknowledged (vmcnt counts stores on gfx9) lane 0 sets the done flag
+// dst[BEVPOOL_META_LEN] the same way, so a host that sees the flag sees the
+// counters -- no event and no cache write-back are needed.
+struct MetaReport {
+  const int32_t *meta = nullptr;
+  int32_t *dst = nullptr;
+};
+
+__device__ __forceinline__ void store_meta_report(const int32_t *__restrict__ meta,
+                                                  int32_t *__restrict__ dst) {
+  if (threadIdx.x < 64) {  // wave 0
+    if (threadIdx.x < BEVPOOL_META_LEN)
+      __hip_atomic_store(dst + threadIdx.x, meta[threadIdx.x], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the counters are acknowledged
+    if (threadIdx.x == 0)
+      __hip_atomic_store(dst + BEVPOOL_META_LEN, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+__device__ __forceinline__ void write_meta_report(const MetaReport &rep) {
+  if (rep.dst && blockIdx.x == 0) store_meta_report(rep.meta, rep.dst);
+}
+
+// bevpool_meta_report: the counters and the done flag, one block of 64.
+__global__ void meta_report_kernel(const int32_t *__restrict__ meta, int32_t *__restrict__ dst) {
+  store_meta_report(meta, dst);
+}
+
 template <typename T, bool kVecRow, bool kVecBev>
 __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
     const float *__restrict__ acc, int C, int CT, const int32_t *__restrict__ cstart,
     const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
-    int64_t sc, int64_t sz, typename T::raw *__restrict__ out) {
+    int64_t sc, int64_t sz, typename T::raw *__restrict__ out, MetaReport report) {
   using raw = typename T::raw;
+  write_meta_report(report);
   extern __shared__ uint32_t tile_bits[];  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
   __shared__ int64_t off[kCellTile];
@@ -2948,7 +2982,7 @@ int launch_forward_pipe(int32_t dtype, const char *x, int64_t ld_bytes, int C, i
 int launch_rows_to_bev(const float *acc, int32_t dtype, int C, const int32_t *cell_start,
                        const int32_t *cell_end, int64_t n_cells, int n_z, int64_t n_xy,
                        int64_t out_stride_b, int64_t out_stride_c, int64_t out_stride_z, void *out,
-                       hipStream_t s) {
+                       hipStream_t s, MetaReport report = {}) {
   if (int st = check_grid(ceil_div(n_cells, kCellTile), kThreads, "cell tiles")) return st;
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
   const int CT = C < kTileChannels ? C : kTileChannels;
@@ -2960,7 +2994,7 @@ int launch_rows_to_bev(const float *acc, int32_t dtype, int C, const int32_t *ce
 #define BEVPOOL_R2B(T, VR, VB)                                                                 \
   hipLaunchKernelGGL((rows_to_bev_kernel<T, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,    \
                      acc, C, CT, cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b,       \
-                     out_stride_c, out_stride_z, static_cast<T::raw *>(out))
+                     out_stride_c, out_stride_z, static_cast<T::raw *>(out), report)
 #define BEVPOOL_R2B_T(T)                                                                       \
   if (vrow && vbev) BEVPOOL_R2B(T, true, true);                                               \
   else if (vrow) BEVPOOL_R2B(T, true, false);                                                 \
@@ -3360,6 +3394,45 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
   return check_launch("cell_ranges");
 }
 
+// Device address for writing to `dst`: pinned host memory through its device
+// address, device memory of the current device as is; anything else
+// (pageable host memory the GPU cannot reach) is refused.
+static int report_address(int32_t *dst, int32_t **dev_dst) {
+  hipPointerAttribute_t a{};
+  if (hipPointerGetAttributes(&a, dst) != hipSuccess) {
+    (void)hipGetLastError();  // unknown pointer: clear the lookup's error
+    return fail(BEVPOOL_EINVAL, "report destination is neither pinned host nor device memory");
+  }
+  if (a.type == hipMemoryTypeHost) {
+    void *d = nullptr;
+    if (hipHostGetDevicePointer(&d, dst, 0) != hipSuccess || !d) {
+      (void)hipGetLastError();
+      return fail(BEVPOOL_EHIP, "hipHostGetDevicePointer failed for the report destination");
+    }
+    *dev_dst = static_cast<int32_t *>(d);
+    return BEVPOOL_OK;
+  }
+  if (a.type == hipMemoryTypeDevice) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != a.device)
+      return fail(BEVPOOL_EINVAL, "report destination on device %d, current device %d",
+                  a.device, dev);
+    *dev_dst = dst;
+    return BEVPOOL_OK;
+  }
+  return fail(BEVPOOL_EINVAL, "report destination is neither pinned host nor device memory");
+}
+
+int bevpool_meta_report(const int32_t *meta, int32_t *dst, void *stream) {
+  g_last_error.clear();
+  if (!meta || !dst) return fail(BEVPOOL_EINVAL, "null meta or destination");
+  int32_t *dev_dst = nullptr;
+  if (int st = report_address(dst, &dev_dst)) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(meta_report_kernel, dim3(1), dim3(64), 0, s, meta, dev_dst);
+  return check_launch("meta_report");
+}
+
 int bevpool_intervals(const uint64_t *keys, int64_t n_points, const int32_t *cell_end,
                       int32_t *starts, int32_t *lengths, int32_t *cells, int32_t *meta,
                       void *workspace, size_t workspace_bytes, void *stream) {
@@ -3401,13 +3474,14 @@ size_t bevpool_forward_scratch_bytes(int64_t n_cells, int32_t C) {
   return size_t(n_cells) * size_t(C) * sizeof(float);
 }
 
-int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
-                    int64_t n_points, const uint64_t *keys, const int32_t *cell_start,
-                    const int32_t *cell_end, const int32_t *meta, int32_t n_batch, int32_t n_z,
-                    int64_t n_xy, int64_t out_stride_b, int64_t out_stride_c,
-                    int64_t out_stride_z, void *out, void *scratch, size_t scratch_bytes,
-                    void *stream) {
-  g_last_error.clear();
+// bevpool_forward; `report` (optional) is written by the transpose's first
+// block.
+static int forward_impl(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                        int64_t n_points, const uint64_t *keys, const int32_t *cell_start,
+                        const int32_t *cell_end, const int32_t *meta, int32_t n_batch,
+                        int32_t n_z, int64_t n_xy, int64_t out_stride_b, int64_t out_stride_c,
+                        int64_t out_stride_z, void *out, void *scratch, size_t scratch_bytes,
+                        void *stream, MetaReport report) {
   if (dtype != BEVPOOL_F32 && dtype != BEVPOOL_F16 && dtype != BEVPOOL_BF16)
     return fail(BEVPOOL_EINVAL, "unsupported dtype code %d", dtype);
   if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
@@ -3464,7 +3538,19 @@ int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, 
     }
   }
   return launch_rows_to_bev(acc, dtype, C, cell_start, cell_end, n_cells, n_z, n_xy,
-                            out_stride_b, out_stride_c, out_stride_z, out, s);
+                            out_stride_b, out_stride_c, out_stride_z, out, s, report);
+}
+
+int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                    int64_t n_points, const uint64_t *keys, const int32_t *cell_start,
+                    const int32_t *cell_end, const int32_t *meta, int32_t n_batch, int32_t n_z,
+                    int64_t n_xy, int64_t out_stride_b, int64_t out_stride_c,
+                    int64_t out_stride_z, void *out, void *scratch, size_t scratch_bytes,
+                    void *stream) {
+  g_last_error.clear();
+  return forward_impl(feats, dtype, feats_row_stride, C, n_points, keys, cell_start, cell_end,
+                      meta, n_batch, n_z, n_xy, out_stride_b, out_stride_c, out_stride_z, out,
+                      scratch, scratch_bytes, stream, MetaReport{});
 }
 
 int bevpool_planar_rows(const float *src, int64_t stride_bn, int64_t stride_c, int32_t BN,
@@ -3865,11 +3951,13 @@ size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C) 
   return op_layout(n_points, n_cells, C).total;
 }
 
-int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
-                       const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
-                       int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W, void *out,
-                       void *workspace, size_t workspace_bytes, void *stream) {
-  g_last_error.clear();
+// bevpool_op_forward with the report destination already resolved to a
+// device address (or null).
+static int op_forward_impl(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                           const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
+                           int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W,
+                           void *out, void *workspace, size_t workspace_bytes,
+                           int32_t *report_dev, void *stream) {
   if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
   if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
   if (n_points < 0 || n_points > int64_t(INT32_MAX))
@@ -3894,9 +3982,26 @@ int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_strid
   if ((st = bevpool_sort(rank, n_points, cells, keys, cstart, cend, meta, iws, iws_bytes, stream)))
     return st;
   const int64_t hw = int64_t(H) * W;
-  return bevpool_forward(feats, dtype, feats_row_stride, C, n_points, keys, cstart, cend, meta, B,
-                         D, hw, int64_t(C) * D * hw, int64_t(D) * hw, hw, out, ws + L.scratch,
-                         size_t(cells) * size_t(C) * sizeof(float), stream);
+  MetaReport rep;
+  rep.meta = meta;
+  rep.dst = report_dev;
+  return forward_impl(feats, dtype, feats_row_stride, C, n_points, keys, cstart, cend, meta, B, D,
+                      hw, int64_t(C) * D * hw, int64_t(D) * hw, hw, out, ws + L.scratch,
+                      size_t(cells) * size_t(C) * sizeof(float), stream, rep);
+}
+
+int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
+                       const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
+                       int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W, void *out,
+                       void *workspace, size_t workspace_bytes, int32_t *report, void *stream) {
+  g_last_error.clear();
+  int32_t *report_dev = nullptr;
+  if (report) {
+    if (int st = report_address(report, &report_dev)) return st;
+  }
+  return op_forward_impl(feats, dtype, feats_row_stride, C, coords, coord_bytes,
+                         coords_row_stride, n_points, B, D, H, W, out, workspace,
+                         workspace_bytes, report_dev, stream);
 }
 
 int bevpool_op_forward_noalloc(const void *feats, int32_t dtype, int64_t feats_row_stride,
@@ -3919,9 +4024,9 @@ int bevpool_op_forward_noalloc(const void *feats, int32_t dtype, int64_t feats_r
   void *ws = noalloc_scratch();
   if (!ws) return BEVPOOL_EHIP;
   g_no_alloc_call = true;
-  const int st = bevpool_op_forward(feats, dtype, feats_row_stride, C, coords, coord_bytes,
-                                    coords_row_stride, n_points, B, D, H, W, out, ws,
-                                    kNoAllocScratchBytes, stream);
+  const int st = op_forward_impl(feats, dtype, feats_row_stride, C, coords, coord_bytes,
+                                 coords_row_stride, n_points, B, D, H, W, out, ws,
+                                 kNoAllocScratchBytes, nullptr, stream);
   g_no_alloc_call = false;
   return st;
 }

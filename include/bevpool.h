@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define BEVPOOL_ABI_VERSION 2
+#define BEVPOOL_ABI_VERSION 3
 
 /* status codes */
 #define BEVPOOL_OK 0
@@ -54,6 +54,8 @@ extern "C" {
 #define BEVPOOL_META_N_BAD 2       /* op-level: coords whose rank is invalid  */
 #define BEVPOOL_META_FIRST_BAD 3   /* op-level: smallest invalid point index  */
 #define BEVPOOL_META_LEN 8
+/* a report destination: the BEVPOOL_META_LEN counters, then a done flag */
+#define BEVPOOL_REPORT_LEN (BEVPOOL_META_LEN + 1)
 
 /* ABI version of the loaded library (BEVPOOL_ABI_VERSION). */
 int bevpool_abi_version(void);
@@ -178,6 +180,22 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
 int bevpool_intervals(const uint64_t *keys, int64_t n_points, const int32_t *cell_end,
                       int32_t *starts, int32_t *lengths, int32_t *cells, int32_t *meta,
                       void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Copies the BEVPOOL_META_LEN counters at `meta` (device memory) to
+ * dst[0 .. BEVPOOL_META_LEN) with one single-block kernel on `stream`, then
+ * sets dst[BEVPOOL_META_LEN] = 1 once they are written, so that a caller
+ * that cleared that flag can poll it and read the counters without a host
+ * synchronisation, an event, a copy engine or a second stream.  `dst`
+ * (BEVPOOL_REPORT_LEN int32) is pinned host memory (hipHostMalloc; written
+ * through its device address with system-scope stores) or device memory of
+ * the current device; anything else is refused with BEVPOOL_EINVAL.
+ *
+ * No reference counterpart: the reference raises out-of-range ranks from its
+ * CPU fallback's index_add_ (ops/bev_pool/src/bev_pool_triton.py:47); this
+ * lets the op-level drop-in report them asynchronously.
+ */
+int bevpool_meta_report(const int32_t *meta, int32_t *dst, void *stream);
 
 /* Bytes of fp32 scratch bevpool_forward needs: n_cells * C * 4. */
 size_t bevpool_forward_scratch_bytes(int64_t n_cells, int32_t C);
@@ -350,13 +368,19 @@ int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t gra
  *   feats        dtype [n_points, C], row stride feats_row_stride, channel stride 1
  *   coords       int32 / int64 (coord_bytes 4 / 8) [n_points, 4] (x, y, z, b)
  *   out          dtype, contiguous (B, C, D, H, W)
+ *   report       NULL, or BEVPOOL_REPORT_LEN int32 of pinned host memory
+ *                (or device memory) that receives a copy of the meta
+ *                counters and then the done flag report[BEVPOOL_META_LEN] = 1,
+ *                written by the call's last kernel (as bevpool_meta_report,
+ *                folded in: no launch of its own): a host that cleared the
+ *                flag polls it and then reads the count of excluded points
  */
 size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C);
 
 int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
                        const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
                        int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W, void *out,
-                       void *workspace, size_t workspace_bytes, void *stream);
+                       void *workspace, size_t workspace_bytes, int32_t *report, void *stream);
 
 /*
  * bevpool_op_forward without a workspace argument, for callers that cannot

@@ -9,6 +9,7 @@ the fp32 reference; fp16/bf16 backward bit-exact (a copy).
 from __future__ import annotations
 
 import json
+import time
 
 import numpy as np
 import pytest
@@ -317,3 +318,34 @@ def test_op_entry_zero_dropped_flag(pkg, cuda):
     P.op_backward(g, 20, 5000, *sizes, xg, ws, zero_dropped=False)
     exp[~keep] = 7.0
     assert_bit_equal(xg, exp, 'zero_dropped = 0')
+
+
+def test_meta_report_entry(pkg, cuda):
+    """bevpool_meta_report through the C ABI: the counters land in pinned
+    host memory, followed by the done flag (polled by the host, no event),
+    and in device memory; pageable host memory, which the GPU cannot reach,
+    is refused before anything is launched."""
+    import ctypes
+
+    from bevfusion_triton_amd import _lib as L
+
+    lib = L.library()
+    meta = torch.arange(100, 100 + L.META_LEN, dtype=torch.int32, device=cuda)
+    s = L.stream_handle(cuda)
+    host = torch.full((3, L.REPORT_LEN), -1, dtype=torch.int32, pin_memory=True)
+    host[1, L.META_LEN] = 0
+    assert lib.bevpool_meta_report(L.ptr(meta), host[1].data_ptr(), s) == 0
+    deadline = time.monotonic() + 10.0
+    while int(host[1, L.META_LEN]) != 1:  # the flag, then the counters
+        assert time.monotonic() < deadline, 'done flag never set'
+        time.sleep(1e-4)
+    assert host[1, :L.META_LEN].tolist() == list(range(100, 100 + L.META_LEN))
+    assert host[0].tolist() == [-1] * L.REPORT_LEN and host[2].tolist() == [-1] * L.REPORT_LEN
+    dev = torch.zeros(L.REPORT_LEN, dtype=torch.int32, device=cuda)
+    assert lib.bevpool_meta_report(L.ptr(meta), L.ptr(dev), s) == 0
+    assert dev.cpu().tolist() == list(range(100, 100 + L.META_LEN)) + [1]
+    pageable = (ctypes.c_int32 * L.REPORT_LEN)()
+    assert lib.bevpool_meta_report(L.ptr(meta), ctypes.addressof(pageable), s) == -1
+    assert list(pageable) == [0] * L.REPORT_LEN
+    assert lib.bevpool_meta_report(L.ptr(meta), 0, s) == -1
+    torch.cuda.synchronize()

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(pkg):
     lib = pkg.library()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.bevpool_abi_version() == 2
+    assert lib.bevpool_abi_version() == 3
     assert lib.bevpool_last_error() == b''
 
 
@@ -159,6 +159,10 @@ def test_status_codes_new_entry_points_without_gpu(pkg):
     ws = np.zeros(1 << 16, np.uint8)
     buf = np.zeros(256, np.float32)
     p = buf.ctypes.data
+    # meta_report: null meta or destination
+    assert lib.bevpool_meta_report(None, p, None) == -1
+    assert lib.bevpool_meta_report(meta.ctypes.data, None, None) == -1
+    assert b'null' in lib.bevpool_last_error()
     # forward_depth: C must be a positive multiple of 4
     st = lib.bevpool_forward_depth(p, p, 6, 0, 1, 1, None, p, p, meta.ctypes.data, 1, 1, 1, 1,
                                    1, 1, p, p, 1 << 20, None)
@@ -215,10 +219,10 @@ def test_op_and_legacy_status_codes(pkg):
     need = lib.bevpool_op_workspace_bytes(1000, 100, 8)
     assert need > 1000 * 12 + 100 * 8 * 4 and need % 256 == 0
     st = lib.bevpool_op_forward(None, 0, 8, 8, None, 4, 4, 1000, 1, 1, 10, 10, None,
-                                ws.ctypes.data, ws.size, None)
+                                ws.ctypes.data, ws.size, None, None)
     assert st == -3 and b'op workspace' in lib.bevpool_last_error()
     st = lib.bevpool_op_forward(None, 0, 8, 8, None, 4, 4, 10, 1, 0, 10, 10, None,
-                                ws.ctypes.data, ws.size, None)
+                                ws.ctypes.data, ws.size, None, None)
     assert st == -1
     st = lib.bevpool_legacy_forward(None, 10, 0, None, None, None, 0, None, 1, 1, 1, 1,
                                     ws.ctypes.data, None, None)
