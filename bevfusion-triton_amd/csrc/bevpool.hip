@@ -76,12 +76,17 @@ namespace {
 // ---------------------------------------------------------------------------
 constexpr int kThreads = 256;              // threads per block, every kernel
 constexpr int kWaves = kThreads / 64;      // wave64 waves per block
-#ifndef BEVPOOL_SORT_ITEMS
-#define BEVPOOL_SORT_ITEMS 8
-#endif
-constexpr int kItems = BEVPOOL_SORT_ITEMS;    // keys per thread in sort kernels
-constexpr int kSortTile = kThreads * kItems;  // keys per sort block
-constexpr int kWaveItems = 64 * kItems;       // keys per wave in the scatter
+// Keys per thread of the sort's tile kernels (quantise / coord ranks, radix
+// histogram and scatter): 8 (tiles of 2048 keys) up to kLargeSortPoints
+// points, 16 (4096) above.  Larger tiles halve the [digit][tile] histogram
+// that every pass writes, scans and reads: at 4 x 360 x 360 and 2 x 720 x 720
+// the forward took 7 and 16 us less on MI355X; at 1 x 360 x 360, whose tiles
+// fill the chip in one round, 3-5 us more.
+constexpr int kItemsSmall = 8, kItemsLarge = 16;
+constexpr int64_t kLargeSortPoints = int64_t(4) << 20;
+inline int sort_items(int64_t n_points) {
+  return n_points > kLargeSortPoints ? kItemsLarge : kItemsSmall;
+}
 constexpr int kMaxDigitBits = 10;
 constexpr int kMaxRadix = 1 << kMaxDigitBits;
 constexpr int kCellTile = 64;              // cells per transpose tile
@@ -123,7 +128,7 @@ inline unsigned xcd_grid(int64_t blocks) {
 #endif
 }
 
-// Grid of a kernel that walks the kSortTile tiles of the sort (at least one
+// Grid of a kernel that walks the tiles of the sort (at least one
 // block: block 0 also resets meta).  Such kernels take tile
 // xcd_chunk(blockIdx.x, gridDim.x), so the 32 tiles that share a 128-byte
 // line of a digit's histogram row are written from one XCD's L2.
@@ -378,13 +383,13 @@ __device__ __forceinline__ int quantize_point(float gx, float gy, float gz, int 
 // points base + 4 * (g * kThreads + tid) + 0..3); with kVec (row stride 3
 // floats, 16-byte aligned base) a group is three 16-byte loads and one
 // 16-byte rank store.  All groups' loads are issued before any is used.
-template <bool kVec>
+template <bool kVec, int kIt>
 __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
     const float *__restrict__ geom, int64_t n_points, int64_t gstride, FastDiv ppb, float o0,
     float o1, float o2, float d0, float d1, float d2, int n0, int n1, int n2,
     int32_t *__restrict__ rank, int32_t *__restrict__ hist, int nblocks, int shift, int bits,
     int32_t *__restrict__ meta) {
-  constexpr int kGroups = kItems / 4;
+  constexpr int kGroups = kIt / 4;
   __shared__ int cnt[kMaxRadix];
   if (blockIdx.x == 0 && threadIdx.x < BEVPOOL_META_LEN)  // nothing else touches meta here
     meta[threadIdx.x] = threadIdx.x == BEVPOOL_META_FIRST_BAD ? 0x7fffffff : 0;
@@ -393,7 +398,7 @@ __global__ __launch_bounds__(kThreads) void quantize_geom_kernel(
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
-  const uint32_t base = uint32_t(tile) * kSortTile;  // n_points < 2^31
+  const uint32_t base = uint32_t(tile) * (kThreads * kIt);  // n_points < 2^31
   const uint32_t n = uint32_t(n_points);
   // raw fp32 bits: lanes of a 16-byte load are never bit cast to float
   // while still in vector form (hipcc 7.2 folded such casts of lanes y/z/w
@@ -548,11 +553,12 @@ __device__ __forceinline__ void frustum_point(const float *__restrict__ c,
 }
 
 // Point p = cam * DHW + f (cam = b*N + n, f = (d*fH + h)*fW + w); frustum
-// fp32 (D, fH, fW, 3) contiguous.  A block takes kSortTile consecutive points
+// fp32 (D, fH, fW, 3) contiguous.  A block takes kThreads * kIt consecutive points
 // (as quantize_geom_kernel, so the pass-0 histograms line up); its first
 // threads build the tables of the cameras it spans in LDS.  A block spanning
 // more than kCamSlots cameras (frustums under ~140 points) builds each
 // point's table in registers instead.
+template <int kIt>
 __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
     const float *__restrict__ frustum, int64_t n_points, FastDiv dhw, FastDiv npb, CameraMats cm,
     float o0,
@@ -570,8 +576,8 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
   const unsigned mask = unsigned(R - 1);
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
   const uint32_t n = uint32_t(n_points);
-  const uint32_t base = uint32_t(tile) * kSortTile;
-  const uint32_t last = (base + kSortTile < n ? base + kSortTile : n) - 1;
+  const uint32_t base = uint32_t(tile) * (kThreads * kIt);
+  const uint32_t last = (base + (kThreads * kIt) < n ? base + (kThreads * kIt) : n) - 1;
   const uint32_t cam_lo = dhw.div(base), cam_hi = dhw.div(last);
   const bool staged = cam_hi - cam_lo < uint32_t(kCamSlots);
   const bool extra = cm.has_extra();
@@ -584,10 +590,10 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
   if (staged) {
     // all frustum loads first (points past n reload point n - 1), then the
     // products; digit counts by runs (every lane active)
-    float fx[kItems], fy[kItems], fz[kItems];
-    uint32_t camv[kItems];
+    float fx[kIt], fy[kIt], fz[kIt];
+    uint32_t camv[kIt];
 #pragma unroll
-    for (int k = 0; k < kItems; ++k) {
+    for (int k = 0; k < kIt; ++k) {
       const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
       const uint32_t pc = p < n ? p : n - 1;
       const uint32_t cam = dhw.div(pc), f = pc - cam * dhw.d;
@@ -597,7 +603,7 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
       fz[k] = frustum[int64_t(f) * 3 + 2];
     }
 #pragma unroll
-    for (int k = 0; k < kItems; ++k) {
+    for (int k = 0; k < kIt; ++k) {
       const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
       const uint32_t c = camv[k] - cam_lo;
       float gx, gy, gz;
@@ -609,7 +615,7 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
     }
   } else {
     // more cameras than LDS slots: each point's tables in registers
-    for (int k = 0; k < kItems; ++k) {
+    for (int k = 0; k < kIt; ++k) {
       const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
       int r = -1;
       if (p < n) {
@@ -631,7 +637,7 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
 }
 
 // ops/bev_pool/src/bev_pool_triton.py:34-39 in int64 (wrapping) arithmetic.
-template <typename TC>
+template <typename TC, int kIt>
 __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
     const TC *__restrict__ coords, int64_t n_points, int64_t cstride, int64_t B, int64_t D,
     int64_t H, int64_t W, int32_t *__restrict__ rank, int32_t *__restrict__ meta,
@@ -643,9 +649,9 @@ __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
   if (tile >= nblocks) return;  // grid padding
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
   __syncthreads();
-  const int64_t base = int64_t(tile) * kSortTile;
+  const int64_t base = int64_t(tile) * (kThreads * kIt);
   const uint64_t cells = uint64_t(B * D * H * W);
-  for (int k = 0; k < kItems; ++k) {
+  for (int k = 0; k < kIt; ++k) {
     const int64_t p = base + int64_t(k) * kThreads + threadIdx.x;
     if (p < n_points) {
       const TC *c = coords + p * cstride;
@@ -708,6 +714,7 @@ __global__ __launch_bounds__(kThreads) void radix_scan_kernel(
 }
 
 // Block histogram of one digit over the sorted keys of the previous pass.
+template <int kIt>
 __global__ __launch_bounds__(kThreads) void radix_hist_kernel(
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
     int32_t *__restrict__ hist, int nblocks, int shift, int bits) {
@@ -719,32 +726,32 @@ __global__ __launch_bounds__(kThreads) void radix_hist_kernel(
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
   __syncthreads();
   const int64_t n = meta[BEVPOOL_META_N_KEPT];
-  const int64_t base = int64_t(tile) * kSortTile;
+  const int64_t base = int64_t(tile) * (kThreads * kIt);
   // all loads first (in bounds: past n they read key 0), then the counts
-  uint64_t key[kItems];
+  uint64_t key[kIt];
 #pragma unroll
-  for (int k = 0; k < kItems; ++k) {
+  for (int k = 0; k < kIt; ++k) {
     const int64_t e = base + int64_t(k) * kThreads + threadIdx.x;
     key[k] = keys[e < n ? e : 0];
   }
 #pragma unroll
-  for (int k = 0; k < kItems; ++k)
+  for (int k = 0; k < kIt; ++k)
     count_digit_runs(cnt, key_digit(key[k], shift, mask),
                      base + int64_t(k) * kThreads + threadIdx.x < n);
   __syncthreads();
   for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + tile] = cnt[d];
 }
 
-// Stable scatter of one LSD radix pass.  Wave w of block b owns the 1024
-// consecutive keys [b*4096 + w*1024, +1024) and walks them 64 at a time in
-// order; a key's destination is
+// Stable scatter of one LSD radix pass.  Wave w of block b owns the 64 * kIt
+// consecutive keys [(b*4 + w) * 64 * kIt, +64 * kIt) and walks them 64 at a
+// time in order; a key's destination is
 //   (keys of smaller digits overall) + (same digit in earlier blocks)
 //   + (same digit in earlier waves of this block) + (same digit earlier in
 //   this wave),
 // the last term from a ballot-built peer mask, so equal digits keep their
 // input order.  Pass 0 (kFromRank) reads int32 ranks in point order, skips
 // dropped points (compaction) and builds the (rank << 32 | point) keys.
-template <bool kFromRank>
+template <bool kFromRank, int kIt>
 __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
     const int32_t *__restrict__ rank_in, const uint64_t *__restrict__ keys_in,
     int64_t n_points, int32_t *__restrict__ meta, uint64_t *__restrict__ keys_out,
@@ -761,16 +768,16 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
   // in the output, so writing them from one XCD lets its L2 merge them into
   // whole lines
   const int tile = int(xcd_chunk(blockIdx.x, gridDim.x));
-  const int64_t blk0 = int64_t(tile) * kSortTile;
+  const int64_t blk0 = int64_t(tile) * (kThreads * kIt);
   if (tile >= nblocks || blk0 >= n) return;  // whole block leaves before any barrier
 
   // this wave's keys, in order (loads issued first so that their latency
   // overlaps the digit-base computation below)
-  uint64_t key[kItems];
-  bool valid[kItems];
-  const int64_t wbase = blk0 + int64_t(w) * kWaveItems;
+  uint64_t key[kIt];
+  bool valid[kIt];
+  const int64_t wbase = blk0 + int64_t(w) * (64 * kIt);
 #pragma unroll
-  for (int k = 0; k < kItems; ++k) {
+  for (int k = 0; k < kIt; ++k) {
     const int64_t e = wbase + k * 64 + lane;
     if (kFromRank) {
       const int r = rank_in[e < n ? e : n - 1];
@@ -806,7 +813,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
   // per-wave digit counts
   int *cnt = s_cnt + w * R;
 #pragma unroll
-  for (int k = 0; k < kItems; ++k) count_digit_runs(cnt, key_digit(key[k], shift, mask), valid[k]);
+  for (int k = 0; k < kIt; ++k) count_digit_runs(cnt, key_digit(key[k], shift, mask), valid[k]);
   __syncthreads();
   for (int d = tid; d < R; d += kThreads) {
     int run = s_base[d];
@@ -821,7 +828,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 
   const uint64_t below_mask = lanes_below();
 #pragma unroll
-  for (int k = 0; k < kItems; ++k) {
+  for (int k = 0; k < kIt; ++k) {
     const unsigned dg = key_digit(key[k], shift, mask);
     const uint64_t peers = peer_mask(dg, valid[k]);
     if (valid[k]) {
@@ -2854,6 +2861,7 @@ DigitPlan plan_digits(int64_t n_cells) {
 struct IndexLayout {
   size_t keys_tmp, hist, totals, bcount, slices, total;
   int64_t sort_blocks, cell_blocks;
+  int items;  // keys per thread of the tile kernels (sort_items)
 };
 
 // Slices of the sliced bucket sort (an upper bound: every group may end in a
@@ -2872,7 +2880,8 @@ size_t slice_count_bytes(int64_t n_points, int64_t n_cells) {
 // caller that only uses the other regions may pass n_cells = 1.
 IndexLayout index_layout(int64_t n_points, int64_t n_cells) {
   IndexLayout L;
-  L.sort_blocks = ceil_div(n_points, kSortTile);
+  L.items = sort_items(n_points);
+  L.sort_blocks = ceil_div(n_points, int64_t(kThreads) * L.items);
   L.cell_blocks = ceil_div(n_points, kThreads);
   size_t o = 0;
   L.keys_tmp = o;
@@ -3239,12 +3248,16 @@ int bevpool_quantize_geom(const float *geom, int64_t n_points, int64_t geom_row_
     const bool vec = geom_row_stride == 3 && n_points >= 4 &&
                      reinterpret_cast<uintptr_t>(geom) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(rank) % 16 == 0;
-#define BEVPOOL_QUANT(V)                                                                       \
-  hipLaunchKernelGGL(quantize_geom_kernel<V>, dim3(grid), dim3(kThreads), 0, s, geom, n_points, \
-                     geom_row_stride, ppb, offset[0], offset[1], offset[2], dx[0],               \
+#define BEVPOOL_QUANT(V, IT)                                                                   \
+  hipLaunchKernelGGL((quantize_geom_kernel<V, IT>), dim3(grid), dim3(kThreads), 0, s, geom,     \
+                     n_points, geom_row_stride, ppb, offset[0], offset[1], offset[2], dx[0],     \
                      dx[1], dx[2], nx[0], nx[1], nx[2], rank, at<int32_t>(workspace, L.hist),   \
                      int(L.sort_blocks), plan.shift[0], plan.bits[0], meta)
-    if (vec) BEVPOOL_QUANT(true); else BEVPOOL_QUANT(false);
+    if (L.items == kItemsLarge) {
+      if (vec) BEVPOOL_QUANT(true, kItemsLarge); else BEVPOOL_QUANT(false, kItemsLarge);
+    } else {
+      if (vec) BEVPOOL_QUANT(true, kItemsSmall); else BEVPOOL_QUANT(false, kItemsSmall);
+    }
 #undef BEVPOOL_QUANT
   }
   return check_launch("quantize_geom");
@@ -3276,12 +3289,15 @@ int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_
   const CameraMats cm{rots, trans, intrins, post_rots, post_trans, extra_rots, extra_trans,
                       n_cams_per_batch};
   LaunchTimer t("quantize_cameras", s);
-  hipLaunchKernelGGL(quantize_frustum_kernel, dim3(sort_grid(L.sort_blocks)), dim3(kThreads), 0, s,
-                     frustum, n_points, make_fast_div(uint32_t(dhw)),
-                     make_fast_div(uint32_t(n_cams_per_batch)), cm, offset[0], offset[1], offset[2],
-                     dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,
-                     at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0], plan.bits[0],
-                     meta);
+#define BEVPOOL_QCAM(IT)                                                                       \
+  hipLaunchKernelGGL((quantize_frustum_kernel<IT>), dim3(sort_grid(L.sort_blocks)),           \
+                     dim3(kThreads), 0, s, frustum, n_points, make_fast_div(uint32_t(dhw)),    \
+                     make_fast_div(uint32_t(n_cams_per_batch)), cm, offset[0], offset[1],      \
+                     offset[2], dx[0], dx[1], dx[2], nx[0], nx[1], nx[2], rank,                \
+                     at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0],        \
+                     plan.bits[0], meta)
+  if (L.items == kItemsLarge) BEVPOOL_QCAM(kItemsLarge); else BEVPOOL_QCAM(kItemsSmall);
+#undef BEVPOOL_QCAM
   return check_launch("quantize_cameras");
 }
 
@@ -3309,19 +3325,20 @@ int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_point
   const IndexLayout L = index_layout(n_points, n_cells);
   const DigitPlan plan = plan_digits(n_cells);
   LaunchTimer t("coord_ranks", s);
+#define BEVPOOL_CRANKS(TC, IT)                                                                 \
+  hipLaunchKernelGGL((coord_ranks_kernel<TC, IT>), dim3(sort_grid(L.sort_blocks)),             \
+                     dim3(kThreads), 0, s, static_cast<const TC *>(coords), n_points,          \
+                     coords_row_stride, int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank,  \
+                     meta, at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0],  \
+                     plan.bits[0])
   if (coord_bytes == 4) {
-    hipLaunchKernelGGL(coord_ranks_kernel<int32_t>, dim3(sort_grid(L.sort_blocks)), dim3(kThreads),
-                       0, s, static_cast<const int32_t *>(coords), n_points, coords_row_stride,
-                       int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
-                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0],
-                       plan.bits[0]);
+    if (L.items == kItemsLarge) BEVPOOL_CRANKS(int32_t, kItemsLarge);
+    else BEVPOOL_CRANKS(int32_t, kItemsSmall);
   } else {
-    hipLaunchKernelGGL(coord_ranks_kernel<int64_t>, dim3(sort_grid(L.sort_blocks)), dim3(kThreads),
-                       0, s, static_cast<const int64_t *>(coords), n_points, coords_row_stride,
-                       int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank, meta,
-                       at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0],
-                       plan.bits[0]);
+    if (L.items == kItemsLarge) BEVPOOL_CRANKS(int64_t, kItemsLarge);
+    else BEVPOOL_CRANKS(int64_t, kItemsSmall);
   }
+#undef BEVPOOL_CRANKS
   return check_launch("coord_ranks");
 }
 
@@ -3351,10 +3368,14 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
   const bool bucketed = plan.local_bits > 0;
   for (int pass = 0; pass < plan.passes; ++pass) {
     uint64_t *dst = bucketed ? tmp : (((plan.passes - 1 - pass) % 2 == 0) ? keys : tmp);
+    const bool large = L.items == kItemsLarge;
     if (pass > 0) {
       LaunchTimer t("radix_hist", s);
-      hipLaunchKernelGGL(radix_hist_kernel, dim3(sort_grid(nb)), dim3(kThreads), 0, s, src, meta, hist, nb,
-                         plan.shift[pass], plan.bits[pass]);
+#define BEVPOOL_RHIST(IT)                                                                      \
+  hipLaunchKernelGGL((radix_hist_kernel<IT>), dim3(sort_grid(nb)), dim3(kThreads), 0, s, src,   \
+                     meta, hist, nb, plan.shift[pass], plan.bits[pass])
+      if (large) BEVPOOL_RHIST(kItemsLarge); else BEVPOOL_RHIST(kItemsSmall);
+#undef BEVPOOL_RHIST
       if ((st = check_launch("radix_hist"))) return st;
     }
     {
@@ -3366,15 +3387,16 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
     }
     {
       LaunchTimer t("radix_scatter", s);
+#define BEVPOOL_RSCAT(FROM_RANK, IT)                                                           \
+  hipLaunchKernelGGL((radix_scatter_kernel<FROM_RANK, IT>), dim3(xcd_grid(nb)), dim3(kThreads), \
+                     0, s, FROM_RANK ? rank : nullptr, FROM_RANK ? nullptr : src, n_points,    \
+                     meta, dst, hist, totals, nb, plan.shift[pass], plan.bits[pass])
       if (pass == 0) {
-        hipLaunchKernelGGL(radix_scatter_kernel<true>, dim3(xcd_grid(nb)), dim3(kThreads), 0, s, rank,
-                           nullptr, n_points, meta, dst, hist, totals, nb, plan.shift[pass],
-                           plan.bits[pass]);
+        if (large) BEVPOOL_RSCAT(true, kItemsLarge); else BEVPOOL_RSCAT(true, kItemsSmall);
       } else {
-        hipLaunchKernelGGL(radix_scatter_kernel<false>, dim3(xcd_grid(nb)), dim3(kThreads), 0, s, nullptr,
-                           src, n_points, meta, dst, hist, totals, nb, plan.shift[pass],
-                           plan.bits[pass]);
+        if (large) BEVPOOL_RSCAT(false, kItemsLarge); else BEVPOOL_RSCAT(false, kItemsSmall);
       }
+#undef BEVPOOL_RSCAT
       if ((st = check_launch("radix_scatter"))) return st;
     }
     src = dst;

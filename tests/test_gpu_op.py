@@ -204,10 +204,16 @@ def test_bucket_sort_edges(pkg, cuda, name, sizes):
     assert_bit_equal(grad, grad32, f'{name} bwd')
 
 
-def test_large_rank_space(pkg, cuda):
-    """2^21 cells: three radix passes."""
+@pytest.mark.parametrize('N', [50000, 4_500_000])
+def test_large_rank_space(pkg, cuda, N):
+    """2^21 cells: three radix passes; with more than 4 Mi points the tile
+    kernels take 4096-key tiles (16 keys per thread)."""
     sizes = (2, 1, 1024, 1024)
-    feats, coords = rand_case(50000, 4, *sizes, seed=9)
+    feats, coords = rand_case(N, 4, *sizes, seed=9)
+    exp = pkg.BevPoolIndexExport(coords.to(cuda), *sizes)
+    perm = ref.sort_perm(ref.flatten_ranks(coords, *sizes))
+    assert torch.equal(exp.perm.cpu(), perm)
+    del exp
     out, grad, up = run_op(pkg, feats, coords, sizes, cuda)
     out32, grad32 = oracle_op(feats, coords, sizes, up)
     assert_bit_equal(out, out32, 'fwd')
