@@ -556,7 +556,9 @@ def access_ceiling(pkg, lib, name, dev):
       * memory_order: cells of 39 consecutive sorted positions whose points are
         consecutive rows, so the rows stream through memory in address order;
       * random_cells: the real cells and chains, cells visited in a random
-        order (identical sums, checked).
+        order (identical sums, checked);
+      * first_point_cells: the same, cells visited in the order of their first
+        point (identical sums, checked).
     Next to them, for scale: torch's own reduction over the whole feature
     tensor (a library read, not a ceiling), a fill and a copy of the same
     size (the copy counts its read and its write), all HIP-event timed
@@ -622,7 +624,20 @@ def access_ceiling(pkg, lib, name, dev):
     keys2 = torch.cat([torch.cat(pieces), idx.keys[n_kept:].cpu()]).to(dev)
     res['random_cells'] = run(keys2, cs2.to(dev), ce2.to(dev))
     res['random_cells']['same_output'] = bool(torch.equal(out, ref_out))
-    for k in ('real', 'memory_order', 'random_cells'):
+    # the real chains, cells visited in the order of their first point
+    first = (k_cpu[cs0[occ]] & 0xFFFFFFFF)
+    order = occ[torch.argsort(first, stable=True)]
+    lens = (ce0 - cs0)[order]
+    starts = torch.cumsum(lens, 0) - lens
+    pieces = [k_cpu[a:b] for a, b in zip(cs0[order].tolist(), ce0[order].tolist())]
+    cs3 = torch.zeros(cells, dtype=torch.int32)
+    ce3 = torch.zeros(cells, dtype=torch.int32)
+    cs3[order] = starts.int()
+    ce3[order] = (starts + lens).int()
+    keys3 = torch.cat([torch.cat(pieces), idx.keys[n_kept:].cpu()]).to(dev)
+    res['first_point_cells'] = run(keys3, cs3.to(dev), ce3.to(dev))
+    res['first_point_cells']['same_output'] = bool(torch.equal(out, ref_out))
+    for k in ('real', 'memory_order', 'random_cells', 'first_point_cells'):
         us = res[k].get('accum_rows')
         if us:
             res[k]['accum_GBps'] = round(res['row_bytes_read'] / (us * 1e-6) / 1e9, 1)
