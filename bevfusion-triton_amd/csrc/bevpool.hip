@@ -991,8 +991,9 @@ constexpr int kSliceKeys = 8192;
 // Groups of 2^kSlicedBits cells take the sliced form.  Smaller groups (at
 // most ~35 K keys measured) take bucket_sort_kernel, whose one launch is
 // faster there (MI355X: 21.6 against 41 us at 1 x 360 x 360, 51 against 74
-// at 4 x 360 x 360); at 2^10 cells per group the sliced form takes 109
-// against 148 us (2 x 720 x 720).
+// at 4 x 360 x 360; sorting one-slice groups in their place block and
+// counting only the others still lost: 30.5 and 63 us); at 2^10 cells per
+// group the sliced form takes 103 against 148 us (2 x 720 x 720).
 constexpr int kSlicedBits = 10;
 constexpr int kSliceWaves = 8;  // 8 waves x 2^10 per-wave digit counts: 32 KB of LDS
 
