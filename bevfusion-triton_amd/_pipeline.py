@@ -9,6 +9,8 @@ and the optional interval export).
 """
 from __future__ import annotations
 
+import threading
+
 import numpy as np
 import torch
 
@@ -386,6 +388,9 @@ class _Pending:
 
 
 _pending = []
+# guards _pending and the slots' free lists: the autograd engine runs
+# backward calls (which poll) on its own threads
+_lock = threading.RLock()
 
 
 class _ReadBack:
@@ -410,20 +415,28 @@ def report_slot(device):
     """A free pinned slot for a deferred report on ``device``, its done flag
     cleared: (state, slot, host address).  Drains the pending reports when
     every slot is taken."""
-    rb = _readback.get(device)
-    if rb is None:
-        rb = _readback[device] = _ReadBack(device)
-    if not rb.free:
-        poll_errors(block=True)  # every slot awaits its kernel: drain them
-    slot = rb.free.pop()
-    rb.view[slot, L.META_LEN] = 0
-    return rb, slot, rb.base + slot * 4 * _ReadBack._STRIDE
+    with _lock:
+        rb = _readback.get(device)
+        if rb is None:
+            rb = _readback[device] = _ReadBack(device)
+        if not rb.free:
+            poll_errors(block=True)  # every slot awaits its kernel: drain them
+        slot = rb.free.pop()
+        rb.view[slot, L.META_LEN] = 0
+        return rb, slot, rb.base + slot * 4 * _ReadBack._STRIDE
+
+
+def release_slot(rb, slot) -> None:
+    """Return a slot whose report was never queued (the call failed)."""
+    with _lock:
+        rb.free.append(slot)
 
 
 def defer_report(rb, slot, report) -> None:
     """Queue ``report(host_meta)`` for slot ``slot``, which work already
     queued on the current stream fills."""
-    _pending.append(_Pending(rb, report, slot))
+    with _lock:
+        _pending.append(_Pending(rb, report, slot))
 
 
 def defer_check(meta, report) -> None:
@@ -439,7 +452,7 @@ def defer_check(meta, report) -> None:
     with torch.cuda.device(device):
         st = L.library().bevpool_meta_report(L.ptr(meta), addr, L.stream_handle(device))
         if st:
-            rb.free.append(slot)
+            release_slot(rb, slot)
         L.check(st, 'bevpool_meta_report')
     defer_report(rb, slot, report)
 
@@ -450,21 +463,26 @@ def poll_errors(block: bool = False) -> None:
     if not _pending:
         return
     if block:
-        for dev in {p.host.device for p in _pending}:
+        with _lock:
+            devices = {p.host.device for p in _pending}
+        for dev in devices:
             torch.cuda.synchronize(dev)
-    done = []
-    keep = []
-    for p in _pending:
-        (done if p.host.view[p.slot, L.META_LEN] else keep).append(p)
-    if not done:
-        return
-    _pending[:] = keep
+    with _lock:
+        done = []
+        keep = []
+        for p in _pending:
+            (done if p.host.view[p.slot, L.META_LEN] else keep).append(p)
+        if not done:
+            return
+        _pending[:] = keep
+        finished = []
+        for p in done:
+            finished.append((p.report, p.host.view[p.slot, :L.META_LEN].copy()))
+            p.host.free.append(p.slot)
     first = None
-    for p in done:
-        meta = p.host.view[p.slot, :L.META_LEN].copy()
-        p.host.free.append(p.slot)
+    for report, meta in finished:
         try:
-            p.report(meta)
+            report(meta)
         except RuntimeError as e:  # report every finished slot; raise the first error
             if first is None:
                 first = e
@@ -522,7 +540,7 @@ def op_forward(feats2d, coords, B, D, H, W, out, ws, report=None) -> None:
             L.stream_handle(device),
         )
         if st and slot is not None:
-            rb.free.append(slot)
+            release_slot(rb, slot)
         L.check(st, 'bevpool_op_forward')
     if slot is not None:
         defer_report(rb, slot, report)

@@ -277,6 +277,50 @@ def test_out_of_range_coords_raise(pkg, cuda):
     assert_bit_equal(out, ref.bev_pool(feats, coords, 1, 2, 3, 4), 'flattened-rank semantics')
 
 
+def test_deferred_reports_from_threads(pkg, cuda):
+    """Op-level calls with deferred bounds reports from several threads at
+    once (the autograd engine polls from its own threads): more calls than
+    pinned report slots, every result exact, every slot returned and no
+    report lost; a bad call afterwards is still reported."""
+    import threading
+
+    from bevfusion_triton_amd import _pipeline as P
+
+    sizes = (1, 2, 9, 11)
+    feats, coords = rand_case(4000, 8, *sizes, seed=31)
+    exp = ref.bev_pool(feats, coords, *sizes)
+    f, c = feats.to(cuda), coords.to(cuda)
+    g = torch.randn(exp.shape, generator=torch.Generator().manual_seed(32)).to(cuda)
+    errors, outs = [], []
+
+    def work():
+        try:
+            for _ in range(40):
+                x = f.clone().requires_grad_(True)
+                out = pkg.bev_pool(x, c, *sizes)
+                (xg,) = torch.autograd.grad(out, x, g)
+            outs.append(out.detach())
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=work) for _ in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    pkg.check_errors()
+    for out in outs:
+        assert_bit_equal(out, exp, 'threaded forward')
+    assert not P._pending
+    assert sorted(P._readback[cuda].free) == list(range(P._ReadBack._SLOTS))
+    bad = coords.clone()
+    bad[5] = torch.tensor([9, 0, 1, 0], dtype=torch.int32)  # x == H at z == D-1
+    pkg.bev_pool(f, bad.to(cuda), *sizes)
+    with pytest.raises(RuntimeError, match='out of bounds'):
+        pkg.check_errors()
+
+
 def test_deterministic(pkg, cuda):
     sizes = (1, 1, 40, 40)
     feats, coords = rand_case(100000, 20, *sizes, seed=8)
