@@ -637,17 +637,28 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
 }
 
 // ops/bev_pool/src/bev_pool_triton.py:34-39 in int64 (wrapping) arithmetic.
-template <typename TC, int kIt>
+// Invalid ranks are counted into meta with atomics (meta initialised by an
+// earlier launch) or, with kTileBad, per tile into tile_bad[tile] (count) and
+// tile_bad[nblocks + tile] (smallest point index, INT32_MAX if none), which
+// the first scatter reduces into meta -- so the op level needs no separate
+// launch to initialise meta.
+template <typename TC, int kIt, bool kTileBad>
 __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
     const TC *__restrict__ coords, int64_t n_points, int64_t cstride, int64_t B, int64_t D,
     int64_t H, int64_t W, int32_t *__restrict__ rank, int32_t *__restrict__ meta,
-    int32_t *__restrict__ hist, int nblocks, int shift, int bits) {
+    int32_t *__restrict__ hist, int nblocks, int shift, int bits,
+    int32_t *__restrict__ tile_bad) {
   __shared__ int cnt[kMaxRadix];
+  __shared__ int s_bad[2];
   const int R = 1 << bits;
   const unsigned mask = unsigned(R - 1);
   const int tile = int(xcd_chunk(blockIdx.x, gridDim.x));
   if (tile >= nblocks) return;  // grid padding
   for (int d = threadIdx.x; d < R; d += kThreads) cnt[d] = 0;
+  if (kTileBad && threadIdx.x == 0) {
+    s_bad[0] = 0;
+    s_bad[1] = INT32_MAX;
+  }
   __syncthreads();
   const int64_t base = int64_t(tile) * (kThreads * kIt);
   const uint64_t cells = uint64_t(B * D * H * W);
@@ -662,6 +673,9 @@ __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
       if (r64 < cells) {  // unsigned compare also rejects negative int64 ranks
         r = int(r64);
         atomicAdd(&cnt[(unsigned(r) >> shift) & mask], 1);
+      } else if (kTileBad) {
+        atomicAdd(&s_bad[0], 1);
+        atomicMin(&s_bad[1], int(p));
       } else {
         atomicAdd(&meta[BEVPOOL_META_N_BAD], 1);
         atomicMin(&meta[BEVPOOL_META_FIRST_BAD], int(p));
@@ -671,6 +685,10 @@ __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
   }
   __syncthreads();
   for (int d = threadIdx.x; d < R; d += kThreads) hist[int64_t(d) * nblocks + tile] = cnt[d];
+  if (kTileBad && threadIdx.x == 0) {
+    tile_bad[tile] = s_bad[0];
+    tile_bad[nblocks + tile] = s_bad[1];
+  }
 }
 
 __global__ void init_meta_kernel(int32_t *meta) {
@@ -756,7 +774,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
     const int32_t *__restrict__ rank_in, const uint64_t *__restrict__ keys_in,
     int64_t n_points, int32_t *__restrict__ meta, uint64_t *__restrict__ keys_out,
     const int32_t *__restrict__ hist, const int32_t *__restrict__ totals, int nblocks,
-    int shift, int bits) {
+    int shift, int bits, const int32_t *__restrict__ tile_bad) {
   __shared__ int s_base[kMaxRadix];
   __shared__ int s_cnt[kWaves * kMaxRadix];
   __shared__ int s_scan[kWaves];
@@ -807,7 +825,44 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
     if (d < R) s_base[d] = ex + hist[int64_t(d) * nblocks + tile];
     ex += loc[i];
   }
-  if (kFromRank && tile == 0 && tid == 0) meta[BEVPOOL_META_N_KEPT] = total;
+  if (kFromRank && tile == 0) {
+    if (tile_bad) {
+      // ranks from coord_ranks_kernel<..., true>: meta was never initialised;
+      // write all of it (kept count, the reduced invalid-rank counters, zeros)
+      int nbad = 0, first = INT32_MAX;
+      for (int t = tid; t < nblocks; t += kThreads) {
+        nbad += tile_bad[t];
+        first = min(first, tile_bad[nblocks + t]);
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        nbad += __shfl_xor(nbad, o, 64);
+        first = min(first, __shfl_xor(first, o, 64));
+      }
+      __shared__ int s_red[2 * kWaves];
+      if (lane == 0) {
+        s_red[w] = nbad;
+        s_red[kWaves + w] = first;
+      }
+      __syncthreads();
+      if (tid < BEVPOOL_META_LEN) {
+        int v = 0;
+        if (tid == BEVPOOL_META_N_KEPT) {
+          v = total;
+        } else if (tid == BEVPOOL_META_N_BAD) {
+#pragma unroll
+          for (int i = 0; i < kWaves; ++i) v += s_red[i];
+        } else if (tid == BEVPOOL_META_FIRST_BAD) {
+          v = INT32_MAX;
+#pragma unroll
+          for (int i = 0; i < kWaves; ++i) v = min(v, s_red[kWaves + i]);
+        }
+        meta[tid] = v;
+      }
+    } else if (tid == 0) {
+      meta[BEVPOOL_META_N_KEPT] = total;
+    }
+  }
   __syncthreads();
 
   // per-wave digit counts
@@ -2860,7 +2915,7 @@ DigitPlan plan_digits(int64_t n_cells) {
 }
 
 struct IndexLayout {
-  size_t keys_tmp, hist, totals, bcount, slices, total;
+  size_t keys_tmp, hist, totals, bcount, tile_bad, slices, total;
   int64_t sort_blocks, cell_blocks;
   int items;  // keys per thread of the tile kernels (sort_items)
 };
@@ -2893,6 +2948,8 @@ IndexLayout index_layout(int64_t n_points, int64_t n_cells) {
   o = align256(o + size_t(kMaxRadix) * sizeof(int32_t));
   L.bcount = o;
   o = align256(o + size_t(L.cell_blocks) * sizeof(int32_t));
+  L.tile_bad = o;  // op level: invalid-rank count and first index per tile
+  o = align256(o + size_t(2) * size_t(L.sort_blocks) * sizeof(int32_t));
   L.slices = o;
   o = align256(o + slice_count_bytes(n_points, n_cells));
   L.total = o;
@@ -3302,11 +3359,13 @@ int bevpool_quantize_cameras(const float *frustum, int32_t D, int32_t fH, int32_
   return check_launch("quantize_cameras");
 }
 
-int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_points,
-                        int64_t coords_row_stride, int32_t B, int32_t D, int32_t H, int32_t W,
-                        int32_t *rank, int32_t *meta, void *workspace, size_t workspace_bytes,
-                        void *stream) {
-  g_last_error.clear();
+// tile_bad: count invalid ranks per tile in the index workspace (for
+// sort_impl's first scatter to reduce into meta) instead of initialising meta
+// here and counting into it with atomics.
+static int coord_ranks_impl(const void *coords, int32_t coord_bytes, int64_t n_points,
+                            int64_t coords_row_stride, int32_t B, int32_t D, int32_t H,
+                            int32_t W, int32_t *rank, int32_t *meta, void *workspace,
+                            size_t workspace_bytes, void *stream, bool tile_bad) {
   if (B < 1 || D < 1 || H < 1 || W < 1)
     return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
   if (coord_bytes != 4 && coord_bytes != 8)
@@ -3317,36 +3376,53 @@ int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_point
   if (n_points > 0 && (!coords || coords_row_stride < 4))
     return fail(BEVPOOL_EINVAL, "bad coords layout");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  {
-    LaunchTimer t("init_meta", s);
-    hipLaunchKernelGGL(init_meta_kernel, dim3(1), dim3(64), 0, s, meta);
+  if (!tile_bad || n_points == 0) {  // no points: no scatter writes meta
+    {
+      LaunchTimer t("init_meta", s);
+      hipLaunchKernelGGL(init_meta_kernel, dim3(1), dim3(64), 0, s, meta);
+    }
+    if ((st = check_launch("init_meta"))) return st;
   }
-  if ((st = check_launch("init_meta"))) return st;
   if (n_points == 0) return BEVPOOL_OK;
   const IndexLayout L = index_layout(n_points, n_cells);
   const DigitPlan plan = plan_digits(n_cells);
+  int32_t *bad = at<int32_t>(workspace, L.tile_bad);
   LaunchTimer t("coord_ranks", s);
-#define BEVPOOL_CRANKS(TC, IT)                                                                 \
-  hipLaunchKernelGGL((coord_ranks_kernel<TC, IT>), dim3(sort_grid(L.sort_blocks)),             \
+#define BEVPOOL_CRANKS(TC, IT, TB)                                                             \
+  hipLaunchKernelGGL((coord_ranks_kernel<TC, IT, TB>), dim3(sort_grid(L.sort_blocks)),         \
                      dim3(kThreads), 0, s, static_cast<const TC *>(coords), n_points,          \
                      coords_row_stride, int64_t(B), int64_t(D), int64_t(H), int64_t(W), rank,  \
                      meta, at<int32_t>(workspace, L.hist), int(L.sort_blocks), plan.shift[0],  \
-                     plan.bits[0])
+                     plan.bits[0], bad)
+#define BEVPOOL_CRANKS_T(TC, IT)                                                               \
+  if (tile_bad) BEVPOOL_CRANKS(TC, IT, true); else BEVPOOL_CRANKS(TC, IT, false);
   if (coord_bytes == 4) {
-    if (L.items == kItemsLarge) BEVPOOL_CRANKS(int32_t, kItemsLarge);
-    else BEVPOOL_CRANKS(int32_t, kItemsSmall);
+    if (L.items == kItemsLarge) { BEVPOOL_CRANKS_T(int32_t, kItemsLarge) }
+    else { BEVPOOL_CRANKS_T(int32_t, kItemsSmall) }
   } else {
-    if (L.items == kItemsLarge) BEVPOOL_CRANKS(int64_t, kItemsLarge);
-    else BEVPOOL_CRANKS(int64_t, kItemsSmall);
+    if (L.items == kItemsLarge) { BEVPOOL_CRANKS_T(int64_t, kItemsLarge) }
+    else { BEVPOOL_CRANKS_T(int64_t, kItemsSmall) }
   }
+#undef BEVPOOL_CRANKS_T
 #undef BEVPOOL_CRANKS
   return check_launch("coord_ranks");
 }
 
-int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_t *keys,
-                 int32_t *cell_start, int32_t *cell_end, int32_t *meta, void *workspace,
-                 size_t workspace_bytes, void *stream) {
+int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_points,
+                        int64_t coords_row_stride, int32_t B, int32_t D, int32_t H, int32_t W,
+                        int32_t *rank, int32_t *meta, void *workspace, size_t workspace_bytes,
+                        void *stream) {
   g_last_error.clear();
+  return coord_ranks_impl(coords, coord_bytes, n_points, coords_row_stride, B, D, H, W, rank,
+                          meta, workspace, workspace_bytes, stream, false);
+}
+
+// tile_bad: the per-tile invalid-rank counts of coord_ranks_impl(...,
+// tile_bad = true) in this workspace; the first scatter then writes all of
+// meta.  nullptr: meta was initialised by the rank kernel's call.
+static int sort_impl(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_t *keys,
+                     int32_t *cell_start, int32_t *cell_end, int32_t *meta, void *workspace,
+                     size_t workspace_bytes, void *stream, bool tile_bad) {
   int st = check_index_args(n_points, n_cells, rank, meta, workspace, workspace_bytes);
   if (st) return st;
   if (!cell_start || !cell_end) return fail(BEVPOOL_EINVAL, "null cell_start/cell_end");
@@ -3391,7 +3467,8 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
 #define BEVPOOL_RSCAT(FROM_RANK, IT)                                                           \
   hipLaunchKernelGGL((radix_scatter_kernel<FROM_RANK, IT>), dim3(xcd_grid(nb)), dim3(kThreads), \
                      0, s, FROM_RANK ? rank : nullptr, FROM_RANK ? nullptr : src, n_points,    \
-                     meta, dst, hist, totals, nb, plan.shift[pass], plan.bits[pass])
+                     meta, dst, hist, totals, nb, plan.shift[pass], plan.bits[pass],           \
+                     FROM_RANK && tile_bad ? at<int32_t>(workspace, L.tile_bad) : nullptr)
       if (pass == 0) {
         if (large) BEVPOOL_RSCAT(true, kItemsLarge); else BEVPOOL_RSCAT(true, kItemsSmall);
       } else {
@@ -3449,6 +3526,14 @@ int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_
                          cell_start, cell_end);
   }
   return check_launch("cell_ranges");
+}
+
+int bevpool_sort(const int32_t *rank, int64_t n_points, int64_t n_cells, uint64_t *keys,
+                 int32_t *cell_start, int32_t *cell_end, int32_t *meta, void *workspace,
+                 size_t workspace_bytes, void *stream) {
+  g_last_error.clear();
+  return sort_impl(rank, n_points, n_cells, keys, cell_start, cell_end, meta, workspace,
+                   workspace_bytes, stream, false);
 }
 
 // Device address for writing to `dst`: pinned host memory through its device
@@ -4033,10 +4118,12 @@ static int op_forward_impl(const void *feats, int32_t dtype, int64_t feats_row_s
   int32_t *cend = reinterpret_cast<int32_t *>(ws + L.cend);
   void *iws = ws + L.index_ws;
   const size_t iws_bytes = index_layout(n_points, cells).total;
-  int st = bevpool_coord_ranks(coords, coord_bytes, n_points, coords_row_stride, B, D, H, W,
-                               rank, meta, iws, iws_bytes, stream);
+  // meta is written by the first scatter (no separate initialising launch)
+  int st = coord_ranks_impl(coords, coord_bytes, n_points, coords_row_stride, B, D, H, W, rank,
+                            meta, iws, iws_bytes, stream, true);
   if (st) return st;
-  if ((st = bevpool_sort(rank, n_points, cells, keys, cstart, cend, meta, iws, iws_bytes, stream)))
+  if ((st = sort_impl(rank, n_points, cells, keys, cstart, cend, meta, iws, iws_bytes, stream,
+                      true)))
     return st;
   const int64_t hw = int64_t(H) * W;
   MetaReport rep;
