@@ -774,7 +774,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
     const int32_t *__restrict__ rank_in, const uint64_t *__restrict__ keys_in,
     int64_t n_points, int32_t *__restrict__ meta, uint64_t *__restrict__ keys_out,
     const int32_t *__restrict__ hist, const int32_t *__restrict__ totals, int nblocks,
-    int shift, int bits, const int32_t *__restrict__ tile_bad) {
+    int shift, int bits, const int32_t *__restrict__ tile_bad, int32_t *__restrict__ gstart) {
   __shared__ int s_base[kMaxRadix];
   __shared__ int s_cnt[kWaves * kMaxRadix];
   __shared__ int s_scan[kWaves];
@@ -808,21 +808,28 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
   }
 
   // digit bases: exclusive scan of the digit totals + this block's prefix
+  // (both loaded before the scan, so their latencies overlap); tile 0's bases
+  // are the digit starts, kept in gstart for the per-group sort
   constexpr int kPer = kMaxRadix / kThreads;  // digits per thread (4)
-  int loc[kPer], tsum = 0;
+  int loc[kPer], pre[kPer], tsum = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int d = tid * kPer + i;
     loc[i] = d < R ? totals[d] : 0;
-    tsum += loc[i];
+    pre[i] = d < R ? hist[int64_t(d) * nblocks + tile] : 0;
   }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) tsum += loc[i];
   for (int d = tid; d < kWaves * R; d += kThreads) s_cnt[d] = 0;
   int total;
   int ex = block_exclusive_scan(tsum, s_scan, &total);
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int d = tid * kPer + i;
-    if (d < R) s_base[d] = ex + hist[int64_t(d) * nblocks + tile];
+    if (d < R) {
+      s_base[d] = ex + pre[i];
+      if (gstart && tile == 0) gstart[d] = ex;
+    }
     ex += loc[i];
   }
   if (kFromRank && tile == 0) {
@@ -918,9 +925,10 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 
 template <int kBucketWaves>
 __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
-    const uint64_t *__restrict__ keys_in, const int32_t *__restrict__ totals, int n_buckets,
-    int64_t n_cells, uint64_t *__restrict__ keys_out, int32_t *__restrict__ cstart,
-    int32_t *__restrict__ cend, int lbits) {
+    const uint64_t *__restrict__ keys_in, const int32_t *__restrict__ totals,
+    const int32_t *__restrict__ gstart, int n_buckets, int64_t n_cells,
+    uint64_t *__restrict__ keys_out, int32_t *__restrict__ cstart, int32_t *__restrict__ cend,
+    int lbits) {
   constexpr int kBucketThreads = 64 * kBucketWaves;
   // sub-batches per load batch: 8 keeps the 16-wave kernel within 64 VGPRs
   // (two blocks per CU); the 8-wave kernel (1024 digits, larger groups)
@@ -936,11 +944,8 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
   const int R = 1 << lbits;
   const unsigned mask = unsigned(R - 1);
 
-  // group start = keys of smaller high digits
-  int part = 0;
-  for (int d = tid; d < bkt; d += kBucketThreads) part += totals[d];
-  int gs;
-  block_exclusive_scan<kBucketWaves>(part, s_scan, &gs);
+  // group start (keys of smaller high digits, from the global pass) and size
+  const int gs = gstart[bkt];
   const int gn = totals[bkt];
   for (int d = tid; d < kBucketWaves * R; d += kBucketThreads) s_cnt[d] = 0;
   const int64_t q = (int64_t(gn) + kBucketThreads - 1) / kBucketThreads * 64;  // keys per wave
@@ -2915,7 +2920,7 @@ DigitPlan plan_digits(int64_t n_cells) {
 }
 
 struct IndexLayout {
-  size_t keys_tmp, hist, totals, bcount, tile_bad, slices, total;
+  size_t keys_tmp, hist, totals, gstart, bcount, tile_bad, slices, total;
   int64_t sort_blocks, cell_blocks;
   int items;  // keys per thread of the tile kernels (sort_items)
 };
@@ -2945,6 +2950,8 @@ IndexLayout index_layout(int64_t n_points, int64_t n_cells) {
   L.hist = o;
   o = align256(o + size_t(kMaxRadix) * size_t(L.sort_blocks) * sizeof(int32_t));
   L.totals = o;
+  o = align256(o + size_t(kMaxRadix) * sizeof(int32_t));
+  L.gstart = o;  // start of each group of the global pass (per-group sort)
   o = align256(o + size_t(kMaxRadix) * sizeof(int32_t));
   L.bcount = o;
   o = align256(o + size_t(L.cell_blocks) * sizeof(int32_t));
@@ -3432,6 +3439,7 @@ static int sort_impl(const int32_t *rank, int64_t n_points, int64_t n_cells, uin
   const DigitPlan plan = plan_digits(n_cells);
   int32_t *hist = at<int32_t>(workspace, L.hist);
   int32_t *totals = at<int32_t>(workspace, L.totals);
+  int32_t *gstart = at<int32_t>(workspace, L.gstart);
   uint64_t *tmp = at<uint64_t>(workspace, L.keys_tmp);
   if (n_points == 0) {
     // no points: only the dense cell ranges need clearing
@@ -3468,7 +3476,8 @@ static int sort_impl(const int32_t *rank, int64_t n_points, int64_t n_cells, uin
   hipLaunchKernelGGL((radix_scatter_kernel<FROM_RANK, IT>), dim3(xcd_grid(nb)), dim3(kThreads), \
                      0, s, FROM_RANK ? rank : nullptr, FROM_RANK ? nullptr : src, n_points,    \
                      meta, dst, hist, totals, nb, plan.shift[pass], plan.bits[pass],           \
-                     FROM_RANK && tile_bad ? at<int32_t>(workspace, L.tile_bad) : nullptr)
+                     FROM_RANK && tile_bad ? at<int32_t>(workspace, L.tile_bad) : nullptr,     \
+                     bucketed ? gstart : nullptr)
       if (pass == 0) {
         if (large) BEVPOOL_RSCAT(true, kItemsLarge); else BEVPOOL_RSCAT(true, kItemsSmall);
       } else {
@@ -3511,7 +3520,7 @@ static int sort_impl(const int32_t *rank, int64_t n_points, int64_t n_cells, uin
     LaunchTimer t("bucket_sort", s);
     const int64_t n_buckets = ceil_div(n_cells, int64_t(1) << plan.local_bits);
     hipLaunchKernelGGL(bucket_sort_kernel<16>, dim3(unsigned(n_buckets)), dim3(16 * 64),
-                       size_t(16) << plan.local_bits << 2, s, src, totals, int(n_buckets),
+                       size_t(16) << plan.local_bits << 2, s, src, totals, gstart, int(n_buckets),
                        n_cells, keys, cell_start, cell_end, plan.local_bits);
     return check_launch("bucket_sort");
   }
