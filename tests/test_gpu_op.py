@@ -145,6 +145,24 @@ def test_shapes_and_edges(pkg, cuda, N, sizes, C):
     assert_bit_equal(grad, grad32, 'bwd')
 
 
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize('C', [90, 136, 200, 264])
+def test_half_channel_blocks(pkg, cuda, dtype, C):
+    """16-bit rows with fp32 sums: one channel block (136), a second partial
+    block beyond the 192 channels one block of 16-bit rows holds (200, 264),
+    and a row size that is not a multiple of 16 bytes (90: the element-wise
+    accumulation).  Forward = the fp32 sum of the same values rounded once;
+    backward = the upstream gradient gathered (a copy)."""
+    sizes = (1, 2, 20, 25)
+    feats, coords = rand_case(6000, C, *sizes, dtype=dtype, seed=C)
+    out, grad, up = run_op(pkg, feats, coords, sizes, cuda)
+    out32, _ = oracle_op(feats.float(), coords, sizes, up)
+    assert out.dtype == dtype
+    assert_bit_equal(out, out32.to(dtype), f'fwd C={C}')
+    _, gref = oracle_op(feats, coords, sizes, up)
+    assert_bit_equal(grad, gref, f'bwd C={C}')
+
+
 @pytest.mark.parametrize('name,sizes', [
     ('11-bit ranks, 2-cell groups', (1, 1, 5, 205)),
     ('20-bit ranks, 1024-cell groups', (1, 1, 1024, 1024)),
