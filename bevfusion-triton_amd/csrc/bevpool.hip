@@ -2559,39 +2559,46 @@ __device__ __forceinline__ void store16(u32x4 *p, u32x4 v) {
 #endif
 }
 
-// Tiled planar -> rows: a block moves 64 consecutive s of one bn, all C
-// channels, through an LDS tile [s][C + 1].  Each 16-lane group loads 256
-// contiguous bytes of one channel (kPer = C / 16 rounded up 16-byte loads per
-// thread, all issued before the tile is written); after one barrier the block
-// writes its 64 rows as one contiguous run of 64 * C floats, 16 bytes per
-// thread, consecutive threads at consecutive addresses (non-temporal).
-// Measured at det (1.28 GB): 248 us against 288 us for the register
-// transpose, whose row stores scatter 16-byte pieces over 16 rows.
+// Tiled planar -> rows: a block moves kPlanarTile consecutive s of one bn,
+// all C channels, through an LDS tile [s][C + 1] (<= 66 KB at C = 128).  Each
+// group of kPlanarTile / 4 lanes loads kPlanarTile * 4 contiguous bytes of one
+// channel (kPer 16-byte loads per thread, all issued before the tile is
+// written); after one barrier the block writes its rows as one contiguous run
+// of kPlanarTile * C floats, 16 bytes per thread, consecutive threads at
+// consecutive addresses (non-temporal).  Measured at det (1.28 GB): 64-point
+// tiles 248 us against 288 us for the register transpose, whose row stores
+// scatter 16-byte pieces over 16 rows; 128-point tiles (512-byte runs per
+// channel) a further -6 us on the channel-first forward.
+#ifndef BEVPOOL_PLANAR_TS
+#define BEVPOOL_PLANAR_TS 128
+#endif
+constexpr int kPlanarTile = BEVPOOL_PLANAR_TS;  // points per tile (64 or 128)
 template <int kPer>
 __global__ __launch_bounds__(kThreads) void planar_tile_kernel(
     const float *__restrict__ src, int C, int64_t S, int64_t tiles_s, int64_t sbn, int64_t sc,
     float *__restrict__ rows) {
-  extern __shared__ float tile[];  // [64][C + 1]
+  constexpr int kQ = kPlanarTile / 4;  // 16-byte pieces per channel of a tile
+  extern __shared__ float tile[];  // [kPlanarTile][C + 1]
   const int pitch = C + 1, tid = threadIdx.x;
   const int64_t bn = int64_t(blockIdx.x) / tiles_s;
-  const int64_t s0 = (int64_t(blockIdx.x) - bn * tiles_s) * 64;
-  const int np = S - s0 < 64 ? int(S - s0) : 64;  // a multiple of 4
+  const int64_t s0 = (int64_t(blockIdx.x) - bn * tiles_s) * kPlanarTile;
+  const int np = S - s0 < kPlanarTile ? int(S - s0) : kPlanarTile;  // a multiple of 4
   const float *in = src + bn * sbn + s0;
-  const int npc = C * 16;  // 16-byte pieces on the channel side
+  const int npc = C * kQ;  // 16-byte pieces on the channel side
   u32x4 v[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     // piece e: channel e / 16, points 4 (e % 16) + [0, 4); pieces past the
     // tile reload an in-bounds one and are not written
     const int e = tid + kThreads * i;
-    const int c = e >> 4, pq = e & 15;
+    const int c = e / kQ, pq = e % kQ;
     const int cc = c < C ? c : C - 1, pp = 4 * pq < np ? pq : 0;
     v[i] = *reinterpret_cast<const u32x4 *>(in + int64_t(cc) * sc + 4 * pp);
   }
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int e = tid + kThreads * i;
-    const int c = e >> 4, pq = e & 15;
+    const int c = e / kQ, pq = e % kQ;
     if (e < npc && 4 * pq < np) {
       float *t = tile + (4 * pq) * pitch + c;
       t[0] = __uint_as_float(v[i].x);
@@ -3716,20 +3723,22 @@ int bevpool_planar_rows(const float *src, int64_t stride_bn, int64_t stride_c, i
                    reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(rows) % 16 == 0;
   LaunchTimer t("planar_rows", s);
-  int st = check_grid(vec ? BN * ceil_div(S, C <= 128 ? 64 : 256) : ceil_div(n_rows * C, kThreads),
+  int st = check_grid(vec ? BN * ceil_div(S, C <= 128 ? kPlanarTile : 256) : ceil_div(n_rows * C, kThreads),
                       kThreads, "planar_rows");
   if (st) return st;
   if (vec && C <= 128) {
-    const int64_t tiles_s = ceil_div(S, 64);
-    const size_t smem = size_t(64) * size_t(C + 1) * sizeof(float);
+    const int64_t tiles_s = ceil_div(S, kPlanarTile);
+    const size_t smem = size_t(kPlanarTile) * size_t(C + 1) * sizeof(float);
 #define BEVPOOL_PT(K)                                                                          \
   case K:                                                                                      \
     hipLaunchKernelGGL((planar_tile_kernel<K>), dim3(unsigned(int64_t(BN) * tiles_s)),          \
                        dim3(kThreads), smem, s, src, C, S, tiles_s, stride_bn, stride_c, rows); \
     break;
-    switch ((C + 15) / 16) {
+    switch ((C * (kPlanarTile / 4) + kThreads - 1) / kThreads) {
       BEVPOOL_PT(1) BEVPOOL_PT(2) BEVPOOL_PT(3) BEVPOOL_PT(4)
       BEVPOOL_PT(5) BEVPOOL_PT(6) BEVPOOL_PT(7) BEVPOOL_PT(8)
+      BEVPOOL_PT(9) BEVPOOL_PT(10) BEVPOOL_PT(11) BEVPOOL_PT(12)
+      BEVPOOL_PT(13) BEVPOOL_PT(14) BEVPOOL_PT(15) BEVPOOL_PT(16)
       default:
         return fail(BEVPOOL_EINVAL, "internal: %d channels on the tiled path", C);
     }
