@@ -209,8 +209,9 @@ def main():
                          "(the traffic calibrator for rocprofv3 --pmc passes), print nothing; "
                          "'configs': fwd/bwd time of every benchmark configuration, one JSON "
                          "line each; 'ceiling': the accumulation kernel on the real index and on "
-                         'synthetic indexes whose rows are read in memory order or in random '
-                         'cell order, next to torch sum/fill/copy rates')
+                         'synthetic indexes whose rows are read in memory order, in random cell '
+                         "order or with the cells in their first point's order, next to torch "
+                         'sum/fill/copy rates')
     ap.add_argument('--fold-pmc', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='fold the counter_collection.csv files of a FETCH_SIZE and a WRITE_SIZE '
                          'pass of --mode kernels into profiles/traffic_<config>.json (no GPU)')
