@@ -295,6 +295,24 @@ def test_out_of_range_coords_raise(pkg, cuda):
     assert_bit_equal(out, ref.bev_pool(feats, coords, 1, 2, 3, 4), 'flattened-rank semantics')
 
 
+def test_deferred_report_on_side_stream(pkg, cuda):
+    """An op-level call queued on a non-default stream: the kernels and the
+    report's done flag go to that stream, so once that stream (and only it)
+    has finished, the out-of-grid coordinate is raised."""
+    feats, coords = rand_case(500, 6, 1, 2, 3, 4, seed=5)
+    coords[123] = torch.tensor([0, 0, 0, 1], dtype=torch.int32)  # b == B
+    keep = torch.arange(500) != 123
+    f, c = feats.to(cuda), coords.to(cuda)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out = pkg.bev_pool(f, c, 1, 2, 3, 4)
+    side.synchronize()
+    assert_bit_equal(out, ref.bev_pool(feats[keep], coords[keep], 1, 2, 3, 4), 'side stream')
+    with pytest.raises(RuntimeError, match='index 24 is out of bounds'):
+        pkg.check_errors()
+
+
 def test_deferred_reports_from_threads(pkg, cuda):
     """Op-level calls with deferred bounds reports from several threads at
     once (the autograd engine polls from its own threads): more calls than
