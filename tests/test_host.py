@@ -37,6 +37,44 @@ def test_library_exports_every_declared_symbol(pkg):
     assert lib.bevpool_last_error() == b''
 
 
+C_CALLER = r"""
+#include <stdio.h>
+#include <string.h>
+#include "bevpool.h"
+int main(void) {
+  if (bevpool_abi_version() != BEVPOOL_ABI_VERSION) return 2;
+  if (bevpool_index_workspace_bytes(1000, 2000) == 0) return 3;
+  /* refused before any HIP call: status and message, as documented */
+  if (bevpool_sort(NULL, 1000, 2000, NULL, NULL, NULL, NULL, NULL, 0, NULL) != BEVPOOL_EINVAL)
+    return 4;
+  if (strlen(bevpool_last_error()) == 0) return 5;
+  puts(bevpool_last_error());
+  return 0;
+}
+"""
+
+
+def test_c_caller_links_and_calls(pkg, tmp_path):
+    """A plain C program (what a cgo / JNI / FFI binding compiles against)
+    includes include/bevpool.h as C99, links the library directly (no torch
+    in the process) and gets the documented status and message."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which('gcc') or shutil.which('cc')
+    if cc is None:
+        pytest.skip('no C compiler')
+    lib = ROOT / 'bevfusion-triton_amd' / 'libbevpool_amd.so'
+    src = tmp_path / 'caller.c'
+    src.write_text(C_CALLER)
+    exe = tmp_path / 'caller'
+    subprocess.run([cc, '-std=c99', '-Wall', '-Werror', f'-I{ROOT / "include"}', str(src), '-o',
+                    str(exe), str(lib), f'-Wl,-rpath,{lib.parent}'], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+    assert r.stdout.strip()
+
+
 def test_workspace_sizes(pkg):
     lib = pkg.library()
     small = lib.bevpool_index_workspace_bytes(1000, 100)
