@@ -459,7 +459,7 @@ def main():
 
 def config_figure(pkg, lib, name, dev):
     """fwd / bwd of one benchmark configuration: median of 20 back-to-back
-    steps by HIP events after 3 warm-ups, the accumulation kernel's average
+    steps by HIP events after 40 warm-ups, the accumulation kernel's average
     by the library's launch events, and the path's algorithmic bandwidth.
     fp32 configurations run the vtransform-level call on the full frustum;
     bf16 runs the op-level bev_pool on the kept points (fp32 accumulation,
@@ -513,7 +513,7 @@ def config_figure(pkg, lib, name, dev):
         fwd_b = s * C * n_kept + s * C * cells
         bwd_b = s * C * n_occ + s * C * n_kept
         level, n_step = 'op', n_kept
-    for _ in range(3):
+    for _ in range(40):  # as the default run: ~10 ms of this load before timing
         bwd(fwd())
     torch.cuda.synchronize()
     evs = []
