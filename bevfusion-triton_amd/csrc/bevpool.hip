@@ -324,6 +324,9 @@ struct F16 {
     *p = __builtin_bit_cast(uint16_t, _Float16(v));
   }
   __device__ static uint16_t to_raw(float v) { return __builtin_bit_cast(uint16_t, _Float16(v)); }
+  __device__ static float from_raw(uint32_t r) {
+    return float(__builtin_bit_cast(_Float16, uint16_t(r)));
+  }
 };
 struct BF16 {
   using raw = uint16_t;
@@ -338,6 +341,7 @@ struct BF16 {
     return uint16_t(u >> 16);
   }
   __device__ static void store(uint16_t *p, float v) { *p = to_raw(v); }
+  __device__ static float from_raw(uint32_t r) { return __builtin_bit_cast(float, r << 16); }
 };
 
 // ---------------------------------------------------------------------------
@@ -1668,37 +1672,55 @@ __device__ __forceinline__ void loader_step(LoaderRing<kSlots> &R, int lt,
 // a chunk with exactly one start at row b jumps (16-way switch) to
 // straight-line code for that b: add rows [0, b), store the finished cell,
 // restart from +0.0, add rows [b, 16); other chunks go row by row.
+// A finished cell row is stored in the output's element type: fp32 for fp32
+// input; for 16-bit input the fp32 sum rounded once (T::to_raw), the value
+// the output gets, so the transpose that follows moves half the bytes.
+// With 16-bit input a lane owns channel pairs instead (pair l + 64 i =
+// channels 2(l + 64 i), +1): one 4-byte LDS read per row and one packed
+// 4-byte store per finished cell; kCPL then counts pairs per lane.
 template <typename T, int kCPL>
 struct RowSum {
-  float a[kCPL];
+  using TO = typename std::conditional<sizeof(typename T::raw) == 2, typename T::raw, float>::type;
+  static constexpr bool kPair = sizeof(typename T::raw) == 2;
+  static constexpr int kA = kPair ? 2 * kCPL : kCPL;  // fp32 accumulators per lane
+  float a[kA];
   int cur = -1;    // rank of the current cell
   int carry = -1;  // rank of the previous stage's last row
 
-  __device__ __forceinline__ void flush(int nch, float *__restrict__ out, int64_t row_elems) {
+  __device__ __forceinline__ void flush(int nch, TO *__restrict__ out, int64_t row_elems) {
     if (cur >= 0) {
-      float *o = out + int64_t(cur) * row_elems;
+      TO *o = out + int64_t(cur) * row_elems;
       const int lane = lane_id();
+      if constexpr (kPair) {
+        uint32_t *o32 = reinterpret_cast<uint32_t *>(o);  // row and channel offsets even
 #pragma unroll
-      for (int i = 0; i < kCPL; ++i)
-        if (lane + 64 * i < nch) o[lane + 64 * i] = a[i];
+        for (int i = 0; i < kCPL; ++i)
+          if (2 * (lane + 64 * i) < nch)
+            o32[lane + 64 * i] =
+                uint32_t(T::to_raw(a[2 * i])) | (uint32_t(T::to_raw(a[2 * i + 1])) << 16);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kCPL; ++i)
+          if (lane + 64 * i < nch) o[lane + 64 * i] = a[i];
+      }
     }
   }
 
   template <int kB, int kStart>
-  __device__ __forceinline__ void split_chunk(const float (&v)[kB][kCPL], int rkl, int j0, int nch,
-                                              float *__restrict__ out, int64_t row_elems) {
+  __device__ __forceinline__ void split_chunk(const float (&v)[kB][kA], int rkl, int j0, int nch,
+                                              TO *__restrict__ out, int64_t row_elems) {
 #pragma unroll
     for (int u = 0; u < kStart; ++u)
 #pragma unroll
-      for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+      for (int i = 0; i < kA; ++i) a[i] += v[u][i];
     flush(nch, out, row_elems);
 #pragma unroll
-    for (int i = 0; i < kCPL; ++i) a[i] = 0.0f;
+    for (int i = 0; i < kA; ++i) a[i] = 0.0f;
     cur = __builtin_amdgcn_readlane(rkl, j0 + kStart);
 #pragma unroll
     for (int u = kStart; u < kB; ++u)
 #pragma unroll
-      for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+      for (int i = 0; i < kA; ++i) a[i] += v[u][i];
   }
 
   // lb: the stage's rows in LDS (row stride cb elements), col: this lane's
@@ -1706,7 +1728,7 @@ struct RowSum {
   __device__ __forceinline__ void add_stage(const typename T::raw *__restrict__ lb,
                                             const int *__restrict__ lrk, int rows, int cb,
                                             const int (&col)[kCPL], int nch,
-                                            float *__restrict__ out, int64_t row_elems) {
+                                            TO *__restrict__ out, int64_t row_elems) {
     const int lane = lane_id();
     const int rkl = lane < rows ? lrk[lane] : -1;
     int prev = __shfl_up(rkl, 1, 64);
@@ -1715,18 +1737,30 @@ struct RowSum {
     if (rows > 0) carry = __builtin_amdgcn_readlane(rkl, rows - 1);
     constexpr int kB = kStageRows < 16 ? kStageRows : 16;
     for (int j0 = 0; j0 < rows; j0 += kB) {
-      float v[kB][kCPL];
+      float v[kB][kA];
+      if constexpr (kPair) {  // col[i]: pair index; cb even
+        const uint32_t *lb32 = reinterpret_cast<const uint32_t *>(lb);
 #pragma unroll
-      for (int u = 0; u < kB; ++u)
+        for (int u = 0; u < kB; ++u)
 #pragma unroll
-        for (int i = 0; i < kCPL; ++i) v[u][i] = T::load(lb + (j0 + u) * cb + col[i]);
+          for (int i = 0; i < kCPL; ++i) {
+            const uint32_t w = lb32[(j0 + u) * (cb >> 1) + col[i]];
+            v[u][2 * i] = T::from_raw(w & 0xffffu);
+            v[u][2 * i + 1] = T::from_raw(w >> 16);
+          }
+      } else {
+#pragma unroll
+        for (int u = 0; u < kB; ++u)
+#pragma unroll
+          for (int i = 0; i < kCPL; ++i) v[u][i] = T::load(lb + (j0 + u) * cb + col[i]);
+      }
       const uint32_t chunk = uint32_t(starts >> j0) & uint32_t((uint64_t(1) << kB) - 1);
       const bool full = j0 + kB <= rows;
       if (full && chunk == 0) {
 #pragma unroll
         for (int u = 0; u < kB; ++u)
 #pragma unroll
-          for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+          for (int i = 0; i < kA; ++i) a[i] += v[u][i];
       } else if (full && (chunk & (chunk - 1)) == 0) {
         switch (__builtin_ctz(chunk)) {
 #define BEVPOOL_SPLIT(B)                                                                       \
@@ -1749,11 +1783,11 @@ struct RowSum {
             if ((chunk >> u) & 1) {
               flush(nch, out, row_elems);
 #pragma unroll
-              for (int i = 0; i < kCPL; ++i) a[i] = 0.0f;
+              for (int i = 0; i < kA; ++i) a[i] = 0.0f;
               cur = __builtin_amdgcn_readlane(rkl, j);
             }
 #pragma unroll
-            for (int i = 0; i < kCPL; ++i) a[i] += v[u][i];
+            for (int i = 0; i < kA; ++i) a[i] += v[u][i];
           }
         }
       }
@@ -1795,17 +1829,27 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
     pr.rowq = cb * int(sizeof(raw)) / 16;
     if (summer) {
       // summing wave `wave` owns channels [wch, wch + nch) of the block
-      const int cps = (cb + kSummers - 1) / kSummers;
+      // (an even count with 16-bit input, whose lanes take channel pairs)
+      constexpr bool kPair = RowSum<T, kCPL>::kPair;
+      int cps = (cb + kSummers - 1) / kSummers;
+      if (kPair) cps += cps & 1;
       const int wch = wave * cps;
       const int nch = cb - wch < cps ? (cb - wch > 0 ? cb - wch : 0) : cps;
       int col[kCPL];
 #pragma unroll
       for (int i = 0; i < kCPL; ++i) {
         const int c = lane_id() + 64 * i;
-        const int cc = wch + (c < nch ? c : (nch > 0 ? nch - 1 : 0));
-        col[i] = cc < cb ? cc : cb - 1;  // idle lanes read a valid column
+        if (kPair) {  // pair index within the stage row
+          const int np = nch >> 1;
+          const int pc = (wch >> 1) + (c < np ? c : (np > 0 ? np - 1 : 0));
+          col[i] = pc < (cb >> 1) ? pc : (cb >> 1) - 1;
+        } else {
+          const int cc = wch + (c < nch ? c : (nch > 0 ? nch - 1 : 0));
+          col[i] = cc < cb ? cc : cb - 1;  // idle lanes read a valid column
+        }
       }
-      float *out = acc + c0 + wch;
+      using TO = typename RowSum<T, kCPL>::TO;  // 16-bit rows for 16-bit input
+      TO *out = reinterpret_cast<TO *>(acc) + c0 + wch;
       RowSum<T, kCPL> st;
       __syncthreads();  // stage 0 is in buffer 0
       for (int k = 0; k < nst; k += kDepth) {  // barriers match the loaders'
@@ -1953,12 +1997,16 @@ __global__ void meta_report_kernel(const int32_t *__restrict__ meta, int32_t *__
   store_meta_report(meta, dst);
 }
 
-template <typename T, bool kVecRow, bool kVecBev>
+// kRaw16: the cell rows already hold the output's 16-bit values (the
+// pipelined accumulation stores them rounded once), moved without conversion;
+// otherwise they are fp32 sums converted on the way out.
+template <typename T, bool kVecRow, bool kVecBev, bool kRaw16 = false>
 __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
     const float *__restrict__ acc, int C, int CT, const int32_t *__restrict__ cstart,
     const int32_t *__restrict__ cend, int64_t n_cells, int n_z, int64_t n_xy, int64_t sb,
     int64_t sc, int64_t sz, typename T::raw *__restrict__ out, MetaReport report) {
   using raw = typename T::raw;
+  static_assert(!kRaw16 || sizeof(raw) == 2, "16-bit rows for 16-bit output only");
   write_meta_report(report);
   extern __shared__ uint32_t tile_bits[];  // kCellTile * (CT + 1)
   __shared__ int occ[kCellTile];
@@ -1990,10 +2038,12 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
     }
     __syncthreads();
   }
+  const uint16_t *acch = reinterpret_cast<const uint16_t *>(acc);
   for (int c0 = 0; c0 < C; c0 += CT) {
     const int cb = C - c0 < CT ? C - c0 : CT;
     if (kVecRow) {
-      const uint32_t q = uint32_t(cb) >> 2;  // 16-byte pieces per row
+      constexpr uint32_t kPer = kRaw16 ? 8 : 4;  // channels per 16-byte piece
+      const uint32_t q = uint32_t(cb) / kPer;    // 16-byte pieces per row
       const uint32_t n_items = kCellTile * q;
       u32x4 v[kTileSlots];
 #pragma unroll
@@ -2001,9 +2051,11 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
         const uint32_t i = tid + it * kThreads;
         uint32_t t = i / q, k = i - t * q;
         if (i >= n_items || cell0 + t >= n_cells) t = k = 0;
-        v[it] = ((occm >> t) & 1)
-                    ? *reinterpret_cast<const u32x4 *>(accb + (cell0 + t) * C + c0 + 4 * k)
-                    : u32x4{0u, 0u, 0u, 0u};
+        const void *src = kRaw16
+                              ? static_cast<const void *>(acch + (cell0 + t) * C + c0 + kPer * k)
+                              : static_cast<const void *>(accb + (cell0 + t) * C + c0 + kPer * k);
+        v[it] = ((occm >> t) & 1) ? *reinterpret_cast<const u32x4 *>(src)
+                                  : u32x4{0u, 0u, 0u, 0u};
       }
       if (c0 == 0 && tid < kCellTile) {
         occ[tid] = occ_mine;
@@ -2014,17 +2066,30 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
         const uint32_t i = tid + it * kThreads;
         if (i < n_items) {
           const uint32_t t = i / q, k = i - t * q;
-          uint32_t *d = tile_bits + t * pitch + 4 * k;
-          d[0] = v[it].x;
-          d[1] = v[it].y;
-          d[2] = v[it].z;
-          d[3] = v[it].w;
+          uint32_t *d = tile_bits + t * pitch + kPer * k;
+          if constexpr (kRaw16) {  // 8 values, low half first
+            d[0] = v[it].x & 0xffffu;
+            d[1] = v[it].x >> 16;
+            d[2] = v[it].y & 0xffffu;
+            d[3] = v[it].y >> 16;
+            d[4] = v[it].z & 0xffffu;
+            d[5] = v[it].z >> 16;
+            d[6] = v[it].w & 0xffffu;
+            d[7] = v[it].w >> 16;
+          } else {
+            d[0] = v[it].x;
+            d[1] = v[it].y;
+            d[2] = v[it].z;
+            d[3] = v[it].w;
+          }
         }
       }
     } else {
       for (uint32_t i = tid; i < uint32_t(kCellTile * cb); i += kThreads) {
         const uint32_t t = i / uint32_t(cb), c = i - t * uint32_t(cb);
-        if (occ[t]) tile_bits[t * pitch + c] = accb[(cell0 + t) * C + c0 + c];
+        if (occ[t])
+          tile_bits[t * pitch + c] = kRaw16 ? uint32_t(acch[(cell0 + t) * C + c0 + c])
+                                            : accb[(cell0 + t) * C + c0 + c];
       }
     }
     __syncthreads();
@@ -2034,7 +2099,10 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const uint32_t b = occ[j + u] ? tile_bits[(j + u) * pitch + c] : 0u;
-        r[u] = T::to_raw(__builtin_bit_cast(float, b));
+        if constexpr (kRaw16)
+          r[u] = raw(b);
+        else
+          r[u] = T::to_raw(__builtin_bit_cast(float, b));
       }
       if (kVecBev) {
         if (off[j] < 0) continue;
@@ -3051,7 +3119,8 @@ int launch_accum_pipe(int32_t dtype, int slots, unsigned grid, size_t smem, hipS
                       const char *x, int64_t ld_bytes, int C, int CB, const uint64_t *keys,
                       const int32_t *meta, const int32_t *cend, float *acc,
                       const DepthRows &dr, bool stream_rows) {
-  const int cpl = pipe_cpl(CB);
+  // summing-lane slots: channels for fp32, channel pairs for 16-bit rows
+  const int cpl = dtype == BEVPOOL_F32 ? pipe_cpl(CB) : pipe_cpl((CB + 1) / 2);
 #define BEVPOOL_PIPE_ARGS                                                                      \
   slots, grid, smem, s, x, ld_bytes, C, CB, keys, meta, cend, acc, dr, stream_rows
 #define BEVPOOL_PIPE_DTYPE(T)                                                                  \
@@ -3097,33 +3166,45 @@ int launch_forward_pipe(int32_t dtype, const char *x, int64_t ld_bytes, int C, i
 int launch_rows_to_bev(const float *acc, int32_t dtype, int C, const int32_t *cell_start,
                        const int32_t *cell_end, int64_t n_cells, int n_z, int64_t n_xy,
                        int64_t out_stride_b, int64_t out_stride_c, int64_t out_stride_z, void *out,
-                       hipStream_t s, MetaReport report = {}) {
+                       hipStream_t s, MetaReport report = {}, bool raw16 = false) {
   if (int st = check_grid(ceil_div(n_cells, kCellTile), kThreads, "cell tiles")) return st;
   const unsigned tiles = unsigned(ceil_div(n_cells, kCellTile));
   const int CT = C < kTileChannels ? C : kTileChannels;
   const size_t es = dtype_size(dtype);
   const size_t smem = size_t(kCellTile) * size_t(CT + 1) * sizeof(uint32_t);
-  const bool vrow = (C % 4 == 0) && (CT % 4 == 0) && (reinterpret_cast<uintptr_t>(acc) % 16 == 0);
+  if (raw16 && es != 2) return fail(BEVPOOL_EINVAL, "internal: 16-bit rows for a 32-bit output");
+  // 16-byte row pieces: 4 fp32 or 8 16-bit channels
+  const int per = raw16 ? 8 : 4;
+  const bool vrow = (C % per == 0) && (CT % per == 0) &&
+                    (reinterpret_cast<uintptr_t>(acc) % 16 == 0);
   const bool vbev = bev_vec_ok(out, es, n_xy, out_stride_b, out_stride_c, out_stride_z);
   LaunchTimer t("rows_to_bev", s);
-#define BEVPOOL_R2B(T, VR, VB)                                                                 \
-  hipLaunchKernelGGL((rows_to_bev_kernel<T, VR, VB>), dim3(tiles), dim3(kThreads), smem, s,    \
-                     acc, C, CT, cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b,       \
+#define BEVPOOL_R2B(T, VR, VB, R16)                                                            \
+  hipLaunchKernelGGL((rows_to_bev_kernel<T, VR, VB, R16>), dim3(tiles), dim3(kThreads), smem,  \
+                     s, acc, C, CT, cell_start, cell_end, n_cells, n_z, n_xy, out_stride_b,    \
                      out_stride_c, out_stride_z, static_cast<T::raw *>(out), report)
-#define BEVPOOL_R2B_T(T)                                                                       \
-  if (vrow && vbev) BEVPOOL_R2B(T, true, true);                                               \
-  else if (vrow) BEVPOOL_R2B(T, true, false);                                                 \
-  else if (vbev) BEVPOOL_R2B(T, false, true);                                                 \
-  else BEVPOOL_R2B(T, false, false);
+#define BEVPOOL_R2B_T(T, R16)                                                                  \
+  if (vrow && vbev) BEVPOOL_R2B(T, true, true, R16);                                          \
+  else if (vrow) BEVPOOL_R2B(T, true, false, R16);                                            \
+  else if (vbev) BEVPOOL_R2B(T, false, true, R16);                                            \
+  else BEVPOOL_R2B(T, false, false, R16);
   switch (dtype) {
     case BEVPOOL_F32:
-      BEVPOOL_R2B_T(F32)
+      BEVPOOL_R2B_T(F32, false)
       break;
     case BEVPOOL_F16:
-      BEVPOOL_R2B_T(F16)
+      if (raw16) {
+        BEVPOOL_R2B_T(F16, true)
+      } else {
+        BEVPOOL_R2B_T(F16, false)
+      }
       break;
     default:
-      BEVPOOL_R2B_T(BF16)
+      if (raw16) {
+        BEVPOOL_R2B_T(BF16, true)
+      } else {
+        BEVPOOL_R2B_T(BF16, false)
+      }
       break;
   }
 #undef BEVPOOL_R2B_T
@@ -3656,6 +3737,7 @@ static int forward_impl(const void *feats, int32_t dtype, int64_t feats_row_stri
   hipStream_t s = static_cast<hipStream_t>(stream);
   float *acc = static_cast<float *>(scratch);
   int st;
+  bool raw16 = false;  // cell rows hold 16-bit output values (pipelined accumulation)
   if (n_points > 0) {
     const size_t es = dtype_size(dtype);
     const bool vec16 = (size_t(C) * es) % 16 == 0 && (size_t(feats_row_stride) * es) % 16 == 0 &&
@@ -3668,6 +3750,7 @@ static int forward_impl(const void *feats, int32_t dtype, int64_t feats_row_stri
                                int64_t(size_t(feats_row_stride) * es), C, n_points, keys, meta,
                                cell_end, acc, DepthRows{nullptr, {}, {}}, s);
       if (st) return st;
+      raw16 = es == 2;
     } else {
       const int CB = C < kThreads ? C : kThreads;
       int R = 8192 / CB;
@@ -3696,7 +3779,7 @@ static int forward_impl(const void *feats, int32_t dtype, int64_t feats_row_stri
     }
   }
   return launch_rows_to_bev(acc, dtype, C, cell_start, cell_end, n_cells, n_z, n_xy,
-                            out_stride_b, out_stride_c, out_stride_z, out, s, report);
+                            out_stride_b, out_stride_c, out_stride_z, out, s, report, raw16);
 }
 
 int bevpool_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
