@@ -8,10 +8,14 @@ the fp32 sums rounded once and within 1e-2 relative of the fp32 reference.
 """
 from __future__ import annotations
 
+import json
+
+import numpy as np
 import pytest
 import torch
 
 from oracle import torch_fallback as ref
+from conftest import GOLDEN
 from test_gpu_op import assert_bit_equal
 
 pytestmark = pytest.mark.gpu
@@ -278,3 +282,38 @@ def test_force_fp32_half_inputs(pkg, cuda, synthetic, dtype, autocast):
     out_ref.backward(g)
     assert_bit_equal(out, out_ref, f'{dtype} x: fp32 forward')
     assert_bit_equal(x.grad, xr.grad.to(dtype), f'{dtype} x: gradient in x dtype')
+
+
+@pytest.mark.parametrize('layout', ['aligned', 'offset', 'batch2'])
+def test_quantize_edges_golden(pkg, cuda, layout):
+    """The quantisation's edge cases (tests/golden/quantize_edges.json, the
+    same vectors the CPU oracles are held to) through the HIP quantise kernel:
+    q in (-1, 0) kept as cell 0, q rounding up to the upper face dropped,
+    height bounds, NaN / +inf / -inf coordinates dropped.  Ranks and kept mask
+    as the vectors state.  Layouts: 16-byte aligned geometry (vector loads), a
+    view starting 12 bytes into its storage (scalar loads), and the points
+    repeated over a batch of 2 (ranks of batch 1 offset by one grid)."""
+    q = json.loads((GOLDEN / 'quantize_edges.json').read_text())
+    g = torch.from_numpy(
+        np.array([p['geom_f32_bits'] for p in q['points']], dtype=np.uint32).view(np.float32))
+    grid = q['grid']
+    dx, bx, nx = ref.gen_dx_bx(grid['xbound'], grid['ybound'], grid['zbound'])
+    want = [p['rank'] for p in q['points']]
+    n_cells = int(nx[0] * nx[1] * nx[2])
+    if layout == 'batch2':
+        geom = torch.stack([g, g]).view(2, 1, 1, 1, -1, 3)
+        want = want + [r + n_cells if r >= 0 else -1 for r in want]
+    else:
+        geom = g.view(1, 1, 1, 1, -1, 3)
+    geom = geom.to(cuda)
+    if layout == 'offset':
+        buf = torch.zeros(geom.numel() + 3, dtype=torch.float32, device=cuda)
+        buf[3:] = geom.reshape(-1)
+        geom = buf[3:].view(geom.shape)
+        assert geom.data_ptr() % 16 == 12
+    exp = pkg.LSSIndexExport(geom, dx, bx, nx)
+    assert exp.rank.cpu().tolist() == want
+    assert exp.kept.cpu().tolist() == [r >= 0 for r in want]
+    kept = [r for r in want if r >= 0]
+    assert exp.sorted_ranks.cpu().tolist() == sorted(kept)
+    assert exp.index.n_points == len(want)
