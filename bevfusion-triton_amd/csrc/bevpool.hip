@@ -666,25 +666,41 @@ __global__ __launch_bounds__(kThreads) void coord_ranks_kernel(
   __syncthreads();
   const int64_t base = int64_t(tile) * (kThreads * kIt);
   const uint64_t cells = uint64_t(B * D * H * W);
-  for (int k = 0; k < kIt; ++k) {
-    const int64_t p = base + int64_t(k) * kThreads + threadIdx.x;
-    if (p < n_points) {
-      const TC *c = coords + p * cstride;
-      const uint64_t x = uint64_t(int64_t(c[0])), y = uint64_t(int64_t(c[1]));
-      const uint64_t z = uint64_t(int64_t(c[2])), b = uint64_t(int64_t(c[3]));
+  // the coordinates of kBatch points per thread are loaded before any is
+  // used (clamped to the last point, so the loads need no branch); the
+  // digits are counted one atomic per run of equal digits
+  constexpr int kBatch = sizeof(TC) == 4 ? 8 : 4;  // 32 VGPRs of coordinates
+  static_assert(kIt % kBatch == 0, "whole batches per thread");
+  for (int k0 = 0; k0 < kIt; k0 += kBatch) {
+    TC cv[kBatch][4];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t p = base + int64_t(k0 + u) * kThreads + threadIdx.x;
+      const TC *c = coords + (p < n_points ? p : n_points - 1) * cstride;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cv[u][j] = c[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t p = base + int64_t(k0 + u) * kThreads + threadIdx.x;
+      const uint64_t x = uint64_t(int64_t(cv[u][0])), y = uint64_t(int64_t(cv[u][1]));
+      const uint64_t z = uint64_t(int64_t(cv[u][2])), b = uint64_t(int64_t(cv[u][3]));
       const uint64_t r64 = ((b * uint64_t(D) + z) * uint64_t(H) + x) * uint64_t(W) + y;
-      int r = -1;
-      if (r64 < cells) {  // unsigned compare also rejects negative int64 ranks
-        r = int(r64);
-        atomicAdd(&cnt[(unsigned(r) >> shift) & mask], 1);
-      } else if (kTileBad) {
-        atomicAdd(&s_bad[0], 1);
-        atomicMin(&s_bad[1], int(p));
-      } else {
-        atomicAdd(&meta[BEVPOOL_META_N_BAD], 1);
-        atomicMin(&meta[BEVPOOL_META_FIRST_BAD], int(p));
+      const bool ok = p < n_points && r64 < cells;  // unsigned: negative ranks fail too
+      const int r = ok ? int(r64) : -1;
+      count_digit_runs(cnt, (unsigned(r) >> shift) & mask, ok);  // every lane takes part
+      if (p < n_points) {
+        if (!ok) {
+          if (kTileBad) {
+            atomicAdd(&s_bad[0], 1);
+            atomicMin(&s_bad[1], int(p));
+          } else {
+            atomicAdd(&meta[BEVPOOL_META_N_BAD], 1);
+            atomicMin(&meta[BEVPOOL_META_FIRST_BAD], int(p));
+          }
+        }
+        rank[p] = r;
       }
-      rank[p] = r;
     }
   }
   __syncthreads();
