@@ -2030,22 +2030,23 @@ __global__ __launch_bounds__(kThreads) void rows_to_bev_kernel(
   (void)cstart;
   const int tid = threadIdx.x;
   const int64_t cell0 = int64_t(blockIdx.x) * kCellTile;
-  int occ_mine = 0;
-  int64_t off_mine = -1;
-  if (tid < kCellTile && cell0 + tid < n_cells) {
-    occ_mine = cend[cell0 + tid] != 0 ? 1 : 0;
-    off_mine = cell_offset(uint32_t(cell0 + tid), uint32_t(n_z), uint32_t(n_xy), sb, sz);
-  }
   const uint32_t *accb = reinterpret_cast<const uint32_t *>(acc);
   const int pitch = CT + 1;
   // occupancy of the tile's 64 cells as a mask in every wave (lane j loads
   // cell j's end), so that only occupied cells' rows are loaded: one more
   // dependent load, and no row bytes for empty cells (most cells of the
-  // sparser grids)
+  // sparser grids); wave 0's mask also gives each cell's own flag, so the
+  // ends are loaded once
   uint64_t occm = 0;
   if (kVecRow) {
     const int64_t cj = cell0 + lane_id();
     occm = __ballot(cj < n_cells && cend[cj] != 0);
+  }
+  int occ_mine = 0;
+  int64_t off_mine = -1;
+  if (tid < kCellTile && cell0 + tid < n_cells) {
+    occ_mine = kVecRow ? int((occm >> tid) & 1u) : (cend[cell0 + tid] != 0 ? 1 : 0);
+    off_mine = cell_offset(uint32_t(cell0 + tid), uint32_t(n_z), uint32_t(n_xy), sb, sz);
   }
   if (!kVecRow) {
     if (tid < kCellTile) {
@@ -2172,8 +2173,6 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
   constexpr int kPer = 16 / int(sizeof(TR));  // elements per 16-byte row piece
   if (kVecBev) {
     (void)cstart;
-    int occ_mine = 0;
-    if (tid < kCellTile && cell0 + tid < n_cells) occ_mine = cend[cell0 + tid] != 0 ? 1 : 0;
     const int j = (tid & 15) * 4;
     const bool live = cell0 + j < n_cells;  // then all 4 cells are (n_cells % 4 == 0)
     const int64_t offj =
@@ -2196,7 +2195,10 @@ __global__ __launch_bounds__(kThreads) void bev_to_rows_kernel(
         c = c < cb ? c : 0;
         v[it] = need ? *reinterpret_cast<const V *>(grad + offj + int64_t(c0 + c) * sc) : V{};
       }
-      if (c0 == 0 && tid < kCellTile) occ[tid] = occ_mine;
+      // the cells' occupancy, loaded after the gradient loads so that one
+      // round trip brings both
+      if (c0 == 0 && tid < kCellTile)
+        occ[tid] = cell0 + tid < n_cells && cend[cell0 + tid] != 0 ? 1 : 0;
 #pragma unroll
       for (int it = 0; it < kTileSlots; ++it) {
         const int c = (tid >> 4) + 16 * it;
