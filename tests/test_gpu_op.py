@@ -145,6 +145,25 @@ def test_shapes_and_edges(pkg, cuda, N, sizes, C):
     assert_bit_equal(grad, grad32, 'bwd')
 
 
+@pytest.mark.parametrize('idx_dtype', [torch.int32, torch.int64])
+@pytest.mark.parametrize('N', [5000, 9001])
+def test_strided_coords(pkg, cuda, idx_dtype, N):
+    """coords as the first four columns of a wider integer tensor (row stride
+    6, passed to the library without a copy), int32 and int64, with a
+    partial last index tile: ranks read through the row stride, forward and
+    backward bit-exact."""
+    sizes = (2, 3, 17, 19)
+    feats, coords = rand_case(N, 8, *sizes, seed=N, idx_dtype=idx_dtype)
+    wide = torch.full((N, 6), 7777, dtype=idx_dtype)
+    wide[:, :4] = coords
+    cw = wide.to(cuda)[:, :4]
+    assert cw.stride() == (6, 1)
+    out, grad, up = run_op(pkg, feats, cw, sizes, cuda)
+    out32, grad32 = oracle_op(feats, coords, sizes, up)
+    assert_bit_equal(out, out32, 'fwd')
+    assert_bit_equal(grad, grad32, 'bwd')
+
+
 @pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize('C', [90, 136, 200, 264])
 def test_half_channel_blocks(pkg, cuda, dtype, C):
