@@ -505,14 +505,32 @@ struct CameraMats {  // fp32, row-major, contiguous per camera / batch
   __device__ __forceinline__ bool has_extra() const { return extra_rots || extra_trans; }
 };
 
-__device__ void camera_table(const CameraMats &m, uint32_t cam, float *__restrict__ t) {
-  const float *R = m.rots + int64_t(cam) * 9, *K = m.intrins + int64_t(cam) * 9;
-  const float *PR = m.post_rots + int64_t(cam) * 9;
+// One camera's inputs, all loaded before any is used (one round trip).
+struct CamIn {
+  float pr[9], pt[3], k[9], r[9], tr[3];
+};
+
+__device__ __forceinline__ void load_camera(const CameraMats &m, uint32_t cam, CamIn &c) {
+  const int64_t o9 = int64_t(cam) * 9, o3 = int64_t(cam) * 3;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) {
+    c.pr[i] = m.post_rots[o9 + i];
+    c.k[i] = m.intrins[o9 + i];
+    c.r[i] = m.rots[o9 + i];
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    c.pt[i] = m.post_trans[o3 + i];
+    c.tr[i] = m.trans[o3 + i];
+  }
+}
+
+__device__ void build_camera_table(const CamIn &c, float *__restrict__ t) {
   for (int i = 0; i < 3; ++i)
-    for (int j = 0; j < 3; ++j) t[3 * i + j] = PR[3 * j + i];  // post_rots^T
-  for (int i = 0; i < 3; ++i) t[9 + i] = m.post_trans[int64_t(cam) * 3 + i];
+    for (int j = 0; j < 3; ++j) t[3 * i + j] = c.pr[3 * j + i];  // post_rots^T
+  for (int i = 0; i < 3; ++i) t[9 + i] = c.pt[i];
   double k[9];
-  for (int i = 0; i < 9; ++i) k[i] = double(K[i]);
+  for (int i = 0; i < 9; ++i) k[i] = double(c.k[i]);
   const double c00 = k[4] * k[8] - k[5] * k[7], c01 = k[5] * k[6] - k[3] * k[8];
   const double c02 = k[3] * k[7] - k[4] * k[6];
   const double det = k[0] * c00 + k[1] * c01 + k[2] * c02;
@@ -523,16 +541,35 @@ __device__ void camera_table(const CameraMats &m, uint32_t cam, float *__restric
   for (int i = 0; i < 3; ++i)
     for (int j = 0; j < 3; ++j) {
       double v = 0.0;
-      for (int q = 0; q < 3; ++q) v += double(R[3 * i + q]) * inv[3 * q + j];
+      for (int q = 0; q < 3; ++q) v += double(c.r[3 * i + q]) * inv[3 * q + j];
       t[12 + 3 * i + j] = float(v);
     }
-  for (int i = 0; i < 3; ++i) t[21 + i] = m.trans[int64_t(cam) * 3 + i];
+  for (int i = 0; i < 3; ++i) t[21 + i] = c.tr[i];
 }
 
-__device__ void batch_table(const CameraMats &m, uint32_t b, float *__restrict__ t) {
-  for (int i = 0; i < 9; ++i)
-    t[i] = m.extra_rots ? m.extra_rots[int64_t(b) * 9 + i] : (i % 4 == 0 ? 1.0f : 0.0f);
-  for (int i = 0; i < 3; ++i) t[9 + i] = m.extra_trans ? m.extra_trans[int64_t(b) * 3 + i] : 0.0f;
+__device__ void camera_table(const CameraMats &m, uint32_t cam, float *__restrict__ t) {
+  CamIn c;
+  load_camera(m, cam, c);
+  build_camera_table(c, t);
+}
+
+// (one branch per pointer, so that the loads are issued together)
+__device__ __forceinline__ void batch_table(const CameraMats &m, uint32_t b,
+                                            float *__restrict__ t) {
+  if (m.extra_rots) {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) t[i] = m.extra_rots[int64_t(b) * 9 + i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) t[i] = i % 4 == 0 ? 1.0f : 0.0f;
+  }
+  if (m.extra_trans) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) t[9 + i] = m.extra_trans[int64_t(b) * 3 + i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) t[9 + i] = 0.0f;
+  }
 }
 
 __device__ __forceinline__ void frustum_point(const float *__restrict__ c,
@@ -585,17 +622,11 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
   const uint32_t cam_lo = dhw.div(base), cam_hi = dhw.div(last);
   const bool staged = cam_hi - cam_lo < uint32_t(kCamSlots);
   const bool extra = cm.has_extra();
-  if (staged && threadIdx.x <= cam_hi - cam_lo) {
-    const uint32_t cam = cam_lo + threadIdx.x;
-    camera_table(cm, cam, lcam[threadIdx.x]);
-    if (extra) batch_table(cm, npb.div(cam), lbat[threadIdx.x]);
-  }
-  __syncthreads();
+  // all frustum loads first (points past n reload point n - 1), issued
+  // before the camera tables are built so that their latencies overlap
+  float fx[kIt], fy[kIt], fz[kIt];
+  uint32_t camv[kIt];
   if (staged) {
-    // all frustum loads first (points past n reload point n - 1), then the
-    // products; digit counts by runs (every lane active)
-    float fx[kIt], fy[kIt], fz[kIt];
-    uint32_t camv[kIt];
 #pragma unroll
     for (int k = 0; k < kIt; ++k) {
       const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
@@ -606,6 +637,22 @@ __global__ __launch_bounds__(kThreads) void quantize_frustum_kernel(
       fy[k] = frustum[int64_t(f) * 3 + 1];
       fz[k] = frustum[int64_t(f) * 3 + 2];
     }
+  }
+  if (staged && threadIdx.x <= cam_hi - cam_lo) {
+    // the camera's and its batch's inputs loaded together, then the tables
+    const uint32_t cam = cam_lo + threadIdx.x;
+    CamIn c;
+    load_camera(cm, cam, c);
+    float e[kBatchFloats];
+    if (extra) batch_table(cm, npb.div(cam), e);
+    build_camera_table(c, lcam[threadIdx.x]);
+    if (extra)
+#pragma unroll
+      for (int i = 0; i < kBatchFloats; ++i) lbat[threadIdx.x][i] = e[i];
+  }
+  __syncthreads();
+  if (staged) {
+    // then the products; digit counts by runs (every lane active)
 #pragma unroll
     for (int k = 0; k < kIt; ++k) {
       const uint32_t p = base + uint32_t(k) * kThreads + threadIdx.x;
