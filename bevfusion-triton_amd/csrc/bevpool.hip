@@ -283,6 +283,34 @@ __device__ __forceinline__ uint64_t peer_mask(unsigned dg, bool valid) {
   return peers;
 }
 
+// Stable rank of this lane's key among the valid lanes of its wave with the
+// same digit (`below`: how many come before it) and their number (`same`).
+// When every lane is valid and the digits are monotone across the lanes (as
+// keys in point order often are), each digit forms one run of lanes and both
+// follow from the run starts: a DPP shift, three ballots and a few bit scans.
+// Otherwise from the peer mask.  Either way the same numbers.  All 64 lanes
+// must be active.
+__device__ __forceinline__ void digit_rank(unsigned dg, bool valid, int &below, int &same) {
+  const int lane = lane_id();
+  const uint64_t le = (uint64_t(2) << lane) - 1;  // lanes <= this one
+  if (__ballot(valid) == ~uint64_t(0)) {
+    // digit of the lane below (lane 0 keeps its own)
+    const unsigned prev =
+        unsigned(__builtin_amdgcn_update_dpp(int(dg), int(dg), 0x138, 0xf, 0xf, false));
+    if (__ballot(dg < prev) == 0 || __ballot(dg > prev) == 0) {
+      const uint64_t heads = __ballot(dg != prev) | uint64_t(1);
+      const int start = 63 - __builtin_clzll(heads & le);
+      const uint64_t after = heads & ~le;
+      below = lane - start;
+      same = (after ? __builtin_ctzll(after) : 64) - start;
+      return;
+    }
+  }
+  const uint64_t peers = peer_mask(dg, valid);
+  below = __popcll(peers & (le >> 1));
+  same = __popcll(peers);
+}
+
 // Exclusive scan of one int per thread across a block of kW waves (256
 // threads by default).  `scratch` holds kW ints.  Every thread must call it.
 template <int kW = kWaves>
@@ -955,16 +983,15 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
   }
   __syncthreads();
 
-  const uint64_t below_mask = lanes_below();
 #pragma unroll
   for (int k = 0; k < kIt; ++k) {
     const unsigned dg = key_digit(key[k], shift, mask);
-    const uint64_t peers = peer_mask(dg, valid[k]);
+    int below, same;
+    digit_rank(dg, valid[k], below, same);
     if (valid[k]) {
-      const int below = __popcll(peers & below_mask);
       const int pos = cnt[dg] + below;
       keys_out[pos] = key[k];
-      if (below == 0) cnt[dg] = pos + __popcll(peers);
+      if (below == 0) cnt[dg] = pos + same;
     }
   }
 }
@@ -1074,7 +1101,6 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
   }
   __syncthreads();
 
-  const uint64_t below_mask = lanes_below();
   for (int e0 = wb; e0 < we; e0 += 64 * kBucketBatch) {
     if (!resident) {
 #pragma unroll
@@ -1089,12 +1115,12 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
       if (e0 + 64 * j >= we) break;
       const bool valid = e0 + 64 * j + lane < we;
       const unsigned dg = key_digit(key[j], 0, mask);
-      const uint64_t peers = peer_mask(dg, valid);
+      int below, same;
+      digit_rank(dg, valid, below, same);
       if (valid) {
-        const int below = __popcll(peers & below_mask);
         const int pos = cnt[dg] + below;
         keys_out[pos] = key[j];
-        if (below == 0) cnt[dg] = pos + __popcll(peers);
+        if (below == 0) cnt[dg] = pos + same;
       }
     }
   }
@@ -1330,18 +1356,17 @@ __global__ __launch_bounds__(64 * kW) void bucket_place_kernel(
     }
   }
   __syncthreads();
-  const uint64_t below_mask = lanes_below();
 #pragma unroll
   for (int j = 0; j < kB; ++j) {
     if (wb + 64 * j >= L.end) break;
     const bool valid = wb + 64 * j + lane < L.end;
     const unsigned dg = key_digit(key[j], 0, mask);
-    const uint64_t peers = peer_mask(dg, valid);
+    int below, same;
+    digit_rank(dg, valid, below, same);
     if (valid) {
-      const int below = __popcll(peers & below_mask);
       const int pos = cnt[dg] + below;
       keys_out[pos] = key[j];
-      if (below == 0) cnt[dg] = pos + __popcll(peers);
+      if (below == 0) cnt[dg] = pos + same;
     }
   }
 }
