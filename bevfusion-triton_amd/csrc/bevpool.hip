@@ -287,7 +287,7 @@ __device__ __forceinline__ uint64_t peer_mask(unsigned dg, bool valid) {
 // same digit (`below`: how many come before it) and their number (`same`).
 // When every lane is valid and the digits are monotone across the lanes (as
 // keys in point order often are), each digit forms one run of lanes and both
-// follow from the run starts: a DPP shift, three ballots and a few bit scans.
+// follow from the run starts: a DPP shift, four ballots and a few bit scans.
 // Otherwise from the peer mask.  Either way the same numbers.  All 64 lanes
 // must be active.
 __device__ __forceinline__ void digit_rank(unsigned dg, bool valid, int &below, int &same) {
@@ -581,7 +581,8 @@ __device__ void camera_table(const CameraMats &m, uint32_t cam, float *__restric
   build_camera_table(c, t);
 }
 
-// (one branch per pointer, so that the loads are issued together)
+// The lidar-augmentation table of batch b (identity when absent), with one
+// branch per pointer so that its loads are issued together.
 __device__ __forceinline__ void batch_table(const CameraMats &m, uint32_t b,
                                             float *__restrict__ t) {
   if (m.extra_rots) {
