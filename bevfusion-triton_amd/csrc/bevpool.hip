@@ -1025,10 +1025,10 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
     uint64_t *__restrict__ keys_out, int32_t *__restrict__ cstart, int32_t *__restrict__ cend,
     int lbits) {
   constexpr int kBucketThreads = 64 * kBucketWaves;
-  // sub-batches per load batch: 8 keeps the 16-wave kernel within 64 VGPRs
-  // (two blocks per CU); the 8-wave kernel (1024 digits, larger groups)
-  // gains from 16
-  constexpr int kBucketBatch = kBucketWaves >= 16 ? 8 : 16;
+  // sub-batches per load batch: 12 keeps the 16-wave kernel within 64 VGPRs
+  // (56; two blocks per CU) and a wave's part of any group up to 12,288 keys
+  // in registers between its two walks (16 spills)
+  constexpr int kBucketBatch = 12;
   extern __shared__ int s_cnt[];  // [kBucketWaves][R]
   __shared__ int s_scan[kBucketWaves];
   // block i takes group i: the large groups (cells near the cameras) are
