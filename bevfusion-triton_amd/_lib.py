@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime first; see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / 'libbevpool_amd.so'
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, F16, BF16 = 0, 1, 2
 META_N_KEPT, META_N_INTERVALS, META_N_BAD, META_FIRST_BAD = 0, 1, 2, 3
@@ -74,10 +74,12 @@ _SIGNATURES = {
          _i32, _vp, _sz, _vp],
         ctypes.c_int,
     ),
+    'bevpool_op_index_bytes': ([_i64, _i64], _sz),
+    'bevpool_op_scratch_bytes': ([_i64, _i64, _i32], _sz),
     'bevpool_op_workspace_bytes': ([_i64, _i64, _i32], _sz),
     'bevpool_op_forward': (
         [_vp, _i32, _i64, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _sz,
-         _vp, _vp],
+         _vp, _sz, _vp, _vp],
         ctypes.c_int,
     ),
     'bevpool_op_forward_noalloc': (
@@ -86,7 +88,7 @@ _SIGNATURES = {
     ),
     'bevpool_op_backward': (
         [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp,
-         _sz, _vp],
+         _sz, _vp, _sz, _vp],
         ctypes.c_int,
     ),
     'bevpool_legacy_forward': (

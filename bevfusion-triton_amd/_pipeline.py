@@ -511,22 +511,38 @@ def coords_report(coords, B, D, H, W):
 
 # ---- one-call op level ------------------------------------------------------
 
-def op_workspace(n_points: int, n_cells: int, C: int, device):
-    nbytes = L.library().bevpool_op_workspace_bytes(n_points, n_cells, C)
+def op_index(n_points: int, n_cells: int, device):
+    """The op-level index buffer (meta counters, ranks, sorted keys, cell
+    ranges): written by :func:`op_forward`, read by :func:`op_backward`."""
+    nbytes = L.library().bevpool_op_index_bytes(n_points, n_cells)
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-def op_meta(ws):
-    """The meta counters at the start of an op-level workspace."""
-    return ws[:4 * L.META_LEN].view(torch.int32)
+def op_scratch(n_points: int, n_cells: int, C: int, device):
+    """Scratch of one op-level call (index-stage workspace and cell rows);
+    enough for the forward and for the backward."""
+    nbytes = L.library().bevpool_op_scratch_bytes(n_points, n_cells, C)
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-def op_forward(feats2d, coords, B, D, H, W, out, ws, report=None) -> None:
-    """The one-call op-level forward.  ``report``: None, or a callable
-    ``report(host_meta)`` run on the meta counters once the device has passed
-    this call (the call's last kernel writes them and a done flag into a
-    pinned slot; no host synchronisation).  Not queued while the stream is
-    being captured."""
+def backward_scratch(n_cells: int, C: int, dtype, device):
+    """Scratch of one backward call (the gradient rows of the cells)."""
+    nbytes = L.library().bevpool_backward_scratch_bytes(n_cells, C, L.DTYPE_CODES[dtype])
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def op_meta(index):
+    """The meta counters at the start of an op-level index buffer."""
+    return index[:4 * L.META_LEN].view(torch.int32)
+
+
+def op_forward(feats2d, coords, B, D, H, W, out, index, scratch, report=None) -> None:
+    """The one-call op-level forward.  ``index`` is kept for the backward;
+    ``scratch`` is needed only during the call.  ``report``: None, or a
+    callable ``report(host_meta)`` run on the meta counters once the device
+    has passed this call (the call's last kernel writes them and a done flag
+    into a pinned slot; no host synchronisation).  Not queued while the
+    stream is being captured."""
     n, C = feats2d.shape
     device = feats2d.device
     slot = None
@@ -536,8 +552,8 @@ def op_forward(feats2d, coords, B, D, H, W, out, ws, report=None) -> None:
         st = L.library().bevpool_op_forward(
             L.ptr(feats2d), L.DTYPE_CODES[feats2d.dtype], feats2d.stride(0) if n else C, C,
             L.ptr(coords), coords.element_size(), coords.stride(0) if n else 4, n, B, D, H,
-            W, L.ptr(out), L.ptr(ws), ws.numel(), addr if slot is not None else None,
-            L.stream_handle(device),
+            W, L.ptr(out), L.ptr(index), index.numel(), L.ptr(scratch), scratch.numel(),
+            addr if slot is not None else None, L.stream_handle(device),
         )
         if st and slot is not None:
             release_slot(rb, slot)
@@ -546,14 +562,14 @@ def op_forward(feats2d, coords, B, D, H, W, out, ws, report=None) -> None:
         defer_report(rb, slot, report)
 
 
-def op_backward(grad, C, n, B, D, H, W, x_grad, ws, zero_dropped=True) -> None:
+def op_backward(grad, C, n, B, D, H, W, x_grad, index, scratch, zero_dropped=True) -> None:
     with torch.cuda.device(grad.device):
         L.check(
             L.library().bevpool_op_backward(
                 L.ptr(grad), L.DTYPE_CODES[grad.dtype], grad.stride(0), grad.stride(1),
                 grad.stride(2), C, n, B, D, H, W, L.ptr(x_grad),
-                x_grad.stride(0) if n else C, 1 if zero_dropped else 0, L.ptr(ws), ws.numel(),
-                L.stream_handle(grad.device),
+                x_grad.stride(0) if n else C, 1 if zero_dropped else 0, L.ptr(index),
+                index.numel(), L.ptr(scratch), scratch.numel(), L.stream_handle(grad.device),
             ),
             'bevpool_op_backward',
         )

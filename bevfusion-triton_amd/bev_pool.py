@@ -16,10 +16,11 @@ Differences from the reference, by design:
     on the device instead of being written out of bounds (the reference's
     Triton path does not check) and reported as the ``RuntimeError`` the CPU
     fallback's ``index_add_`` raises.  By default the report is asynchronous:
-    the device counters are copied behind an event and the error is raised
-    by the next call of this module's functions once the device has passed
-    that point (or by :func:`check_errors`), so a call never waits for the
-    device.  ``check_bounds='sync'`` waits and raises in the same call;
+    the forward's last kernel writes the device counters into a slot of
+    pinned host memory and then sets the slot's done flag; the next call of
+    this module's functions (or :func:`check_errors`) polls that flag and
+    raises once it is set, so a call never waits for the device.
+    ``check_bounds='sync'`` waits and raises in the same call;
     ``check_bounds=False`` drops such points silently;
   * CPU tensors are rejected: the HIP path is the only implementation.
 """
@@ -63,8 +64,10 @@ class BevPoolFunction(torch.autograd.Function):
     forward pools straight into the channel-first (B, C, D, H, W) layout (the
     reference's ``permute().contiguous()`` of ``:227`` is fused into the
     kernel's store) with one call of the library's op-level entry, which
-    leaves the index in its workspace for the backward; backward returns
-    ``(x_grad, None x 6)``."""
+    leaves the index (ranks, sorted keys, cell ranges: 12 bytes per point
+    plus 8 per cell) in a buffer saved for the backward; the call's scratch
+    (index-stage workspace and cell rows) is freed after each call.  Backward
+    returns ``(x_grad, None x 6)``."""
 
     @staticmethod
     def forward(ctx, feats, coords, B, D, H, W, check_bounds=True):
@@ -74,22 +77,23 @@ class BevPoolFunction(torch.autograd.Function):
         ctx.feats_meta = (N, C, feats.dtype)
         ctx.sizes = (B, D, H, W)
         if C == 0:  # nothing to pool; the reference returns an empty (B, 0, D, H, W)
-            ctx.ws = None
+            ctx.index = None
             return feats.new_zeros((B, 0, D, H, W))
         P._check_sizes(N, B * D * H * W)
         feats2d = feats if feats.stride(1) == 1 or N == 0 else feats.contiguous()
         coords2d = coords if coords.stride(1) == 1 or N == 0 else coords.contiguous()
-        ws = P.op_workspace(N, B * D * H * W, C, feats.device)
+        index = P.op_index(N, B * D * H * W, feats.device)
+        scratch = P.op_scratch(N, B * D * H * W, C, feats.device)
         out = torch.empty((B, C, D, H, W), dtype=feats.dtype, device=feats.device)
         if check_bounds == 'sync':
-            P.op_forward(feats2d, coords2d, B, D, H, W, out, ws)
-            P.coords_report(coords2d, B, D, H, W)(P.op_meta(ws).cpu().numpy())
+            P.op_forward(feats2d, coords2d, B, D, H, W, out, index, scratch)
+            P.coords_report(coords2d, B, D, H, W)(P.op_meta(index).cpu().numpy())
         elif check_bounds:
-            P.op_forward(feats2d, coords2d, B, D, H, W, out, ws,
+            P.op_forward(feats2d, coords2d, B, D, H, W, out, index, scratch,
                          report=P.coords_report(coords2d, B, D, H, W))
         else:
-            P.op_forward(feats2d, coords2d, B, D, H, W, out, ws)
-        ctx.ws = ws
+            P.op_forward(feats2d, coords2d, B, D, H, W, out, index, scratch)
+        ctx.index = index
         return out
 
     @staticmethod
@@ -97,7 +101,7 @@ class BevPoolFunction(torch.autograd.Function):
         P.poll_errors()
         N, C, dtype = ctx.feats_meta
         B, D, H, W = ctx.sizes
-        if ctx.ws is None:
+        if ctx.index is None:
             return out_grad.new_zeros((N, C), dtype=dtype), None, None, None, None, None, None
         g = out_grad
         if g.dtype != dtype:
@@ -105,7 +109,8 @@ class BevPoolFunction(torch.autograd.Function):
         if g.stride(4) != 1 or g.stride(3) != W:
             g = g.contiguous()
         x_grad = torch.empty((N, C), dtype=dtype, device=g.device)
-        P.op_backward(g, C, N, B, D, H, W, x_grad, ctx.ws)
+        scratch = P.backward_scratch(B * D * H * W, C, dtype, g.device)
+        P.op_backward(g, C, N, B, D, H, W, x_grad, ctx.index, scratch)
         return x_grad, None, None, None, None, None, None
 
 

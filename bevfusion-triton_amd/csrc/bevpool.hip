@@ -1576,7 +1576,7 @@ __global__ __launch_bounds__(kThreads) void accum_rows_kernel(
 #ifndef BEVPOOL_DEPTH
 #define BEVPOOL_DEPTH 2
 #endif
-constexpr int kStageRows = BEVPOOL_STAGE_ROWS;  // sorted points per stage (power of 2, <= 64)
+constexpr int kStageRows = BEVPOOL_STAGE_ROWS;  // sorted points per stage
 constexpr int kDepth = BEVPOOL_DEPTH;           // row stages in flight per loader thread
 #ifndef BEVPOOL_SUMMERS
 #define BEVPOOL_SUMMERS 1
@@ -1587,7 +1587,11 @@ constexpr int kDepth = BEVPOOL_DEPTH;           // row stages in flight per load
 constexpr int kSummers = BEVPOOL_SUMMERS;       // summing waves (waves 0..kSummers-1)
 constexpr int kLoaders = 64 * BEVPOOL_LOADER_WAVES;  // loader threads (the other waves)
 constexpr int kPipeThreads = 64 * kSummers + kLoaders;
-static_assert(kStageRows <= 64 && (kStageRows & (kStageRows - 1)) == 0, "stage rows");
+// Only 32-row stages are built and tested.  A 64-row variant built with
+// -DBEVPOOL_STAGE_ROWS=64 failed one camera-index parity case on MI355X and
+// passed it on the next run, without a cause found; 16-row stages were only
+// ever timed.  Other values are therefore refused at compile time.
+static_assert(kStageRows == 32, "only 32-row accumulation stages are supported");
 
 // native 16-byte vector (register-promotable, unlike the HIP uint4 wrapper)
 
@@ -2056,10 +2060,10 @@ constexpr int64_t kOccFirstCells = 200000;
 
 // Optional copy of the meta counters into memory the host reads (pinned host
 // memory through its device address), made by a kernel that runs anyway.
-// The counters go out as system-scope (written-through) stores; once they
-// are acknowledged (vmcnt counts stores on gfx9) lane 0 sets the done flag
-// dst[BEVPOOL_META_LEN] the same way, so a host that sees the flag sees the
-// counters -- no event and no cache write-back are needed.
+// One thread writes the counters as system-scope stores and then sets the
+// done flag dst[BEVPOOL_META_LEN] with a system-scope release store, so a
+// host that sees the flag sees the counters (the release orders the
+// thread's earlier stores before the flag; no event is involved).
 struct MetaReport {
   const int32_t *meta = nullptr;
   int32_t *dst = nullptr;
@@ -2067,13 +2071,14 @@ struct MetaReport {
 
 __device__ __forceinline__ void store_meta_report(const int32_t *__restrict__ meta,
                                                   int32_t *__restrict__ dst) {
-  if (threadIdx.x < 64) {  // wave 0
-    if (threadIdx.x < BEVPOOL_META_LEN)
-      __hip_atomic_store(dst + threadIdx.x, meta[threadIdx.x], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_SYSTEM);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the counters are acknowledged
-    if (threadIdx.x == 0)
-      __hip_atomic_store(dst + BEVPOOL_META_LEN, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (threadIdx.x == 0) {
+    int32_t v[BEVPOOL_META_LEN];
+#pragma unroll
+    for (int i = 0; i < BEVPOOL_META_LEN; ++i) v[i] = meta[i];
+#pragma unroll
+    for (int i = 0; i < BEVPOOL_META_LEN; ++i)
+      __hip_atomic_store(dst + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(dst + BEVPOOL_META_LEN, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -2081,7 +2086,8 @@ __device__ __forceinline__ void write_meta_report(const MetaReport &rep) {
   if (rep.dst && blockIdx.x == 0) store_meta_report(rep.meta, rep.dst);
 }
 
-// bevpool_meta_report: the counters and the done flag, one block of 64.
+// bevpool_meta_report: the counters and the done flag, one block of 64 (its
+// first thread does the work).
 __global__ void meta_report_kernel(const int32_t *__restrict__ meta, int32_t *__restrict__ dst) {
   store_meta_report(meta, dst);
 }
@@ -3377,15 +3383,16 @@ int check_legacy_args(int64_t n, int32_t C, const void *geom, const void *starts
   return BEVPOOL_OK;
 }
 
-// Layout of the op-level workspace (bevpool_op_forward / bevpool_op_backward):
-// meta, the index (ranks, sorted keys, cell ranges), the index-stage
-// workspace and the cell-row scratch shared by the forward and the backward.
-struct OpLayout {
-  size_t meta, rank, keys, cstart, cend, index_ws, scratch, total;
+// Layout of the op-level buffers (bevpool_op_forward / bevpool_op_backward).
+// The index buffer keeps what the backward needs: meta, ranks, sorted keys and
+// cell ranges.  The scratch buffer holds the index-stage workspace and the
+// cell rows; it is needed only during a call.
+struct OpIndexLayout {
+  size_t meta, rank, keys, cstart, cend, total;
 };
 
-OpLayout op_layout(int64_t n, int64_t cells, int32_t C) {
-  OpLayout L;
+OpIndexLayout op_index_layout(int64_t n, int64_t cells) {
+  OpIndexLayout L;
   size_t o = 0;
   L.meta = o;
   o = align256(o + BEVPOOL_META_LEN * sizeof(int32_t));
@@ -3397,16 +3404,28 @@ OpLayout op_layout(int64_t n, int64_t cells, int32_t C) {
   o = align256(o + size_t(cells) * sizeof(int32_t));
   L.cend = o;
   o = align256(o + size_t(cells) * sizeof(int32_t));
+  L.total = o;
+  return L;
+}
+
+struct OpScratchLayout {
+  size_t index_ws, rows, total;
+};
+
+OpScratchLayout op_scratch_layout(int64_t n, int64_t cells, int32_t C) {
+  OpScratchLayout L;
+  size_t o = 0;
   L.index_ws = o;
   o = align256(o + index_layout(n, cells).total);
-  L.scratch = o;
+  L.rows = o;
   o = align256(o + size_t(cells) * size_t(C) * sizeof(float));
   L.total = o;
   return L;
 }
 
-// Scratch of the allocation-free op-level forward: the whole op workspace
-// (op_layout) of one call lives in this array, one copy per GPU, held until
+// Scratch of the allocation-free op-level forward: the index buffer
+// (op_index_layout) and the scratch (op_scratch_layout) of one call live in
+// this array, one copy per GPU, held until
 // the process ends.  Host code never passes `scratch` itself to a kernel or
 // a copy (in host code the name is a host-side stand-in, not a device
 // address): it uses the device address hipGetSymbolAddress returns for the
@@ -4280,9 +4299,17 @@ int bevpool_runs(const void *ranks, int32_t rank_bytes, int64_t n, int32_t *star
   return check_launch("run_length");
 }
 
-size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C) {
-  if (n_points < 0 || n_cells < 0 || C < 0) return 0;
-  return op_layout(n_points, n_cells, C).total;
+
+// Checks shared by the op-level entry points.
+static int op_check_sizes(int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W,
+                          int32_t C) {
+  if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
+  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
+  if (n_points < 0 || n_points > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range", (long long)n_points);
+  if (int64_t(B) * D * H * W > int64_t(INT32_MAX))
+    return fail(BEVPOOL_EINVAL, "B*D*H*W exceeds 2^31-1");
+  return BEVPOOL_OK;
 }
 
 // bevpool_op_forward with the report destination already resolved to a
@@ -4290,25 +4317,25 @@ size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C) 
 static int op_forward_impl(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
                            const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
                            int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W,
-                           void *out, void *workspace, size_t workspace_bytes,
-                           int32_t *report_dev, void *stream) {
-  if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
-  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
-  if (n_points < 0 || n_points > int64_t(INT32_MAX))
-    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range", (long long)n_points);
+                           void *out, void *index, size_t index_bytes, void *scratch,
+                           size_t scratch_bytes, int32_t *report_dev, void *stream) {
+  if (int st = op_check_sizes(n_points, B, D, H, W, C)) return st;
   const int64_t cells = int64_t(B) * D * H * W;
-  if (cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "B*D*H*W exceeds 2^31-1");
-  if (!workspace) return fail(BEVPOOL_EINVAL, "null workspace");
-  const OpLayout L = op_layout(n_points, cells, C);
-  if (workspace_bytes < L.total)
-    return fail(BEVPOOL_ESPACE, "op workspace %zu bytes < required %zu", workspace_bytes, L.total);
-  char *ws = static_cast<char *>(workspace);
-  int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
-  int32_t *rank = reinterpret_cast<int32_t *>(ws + L.rank);
-  uint64_t *keys = reinterpret_cast<uint64_t *>(ws + L.keys);
-  int32_t *cstart = reinterpret_cast<int32_t *>(ws + L.cstart);
-  int32_t *cend = reinterpret_cast<int32_t *>(ws + L.cend);
-  void *iws = ws + L.index_ws;
+  if (!index || !scratch) return fail(BEVPOOL_EINVAL, "null index or scratch buffer");
+  const OpIndexLayout L = op_index_layout(n_points, cells);
+  if (index_bytes < L.total)
+    return fail(BEVPOOL_ESPACE, "op index buffer %zu bytes < required %zu", index_bytes, L.total);
+  const OpScratchLayout S = op_scratch_layout(n_points, cells, C);
+  if (scratch_bytes < S.total)
+    return fail(BEVPOOL_ESPACE, "op scratch %zu bytes < required %zu", scratch_bytes, S.total);
+  char *ix = static_cast<char *>(index);
+  char *sc = static_cast<char *>(scratch);
+  int32_t *meta = reinterpret_cast<int32_t *>(ix + L.meta);
+  int32_t *rank = reinterpret_cast<int32_t *>(ix + L.rank);
+  uint64_t *keys = reinterpret_cast<uint64_t *>(ix + L.keys);
+  int32_t *cstart = reinterpret_cast<int32_t *>(ix + L.cstart);
+  int32_t *cend = reinterpret_cast<int32_t *>(ix + L.cend);
+  void *iws = sc + S.index_ws;
   const size_t iws_bytes = index_layout(n_points, cells).total;
   // meta is written by the first scatter (no separate initialising launch)
   int st = coord_ranks_impl(coords, coord_bytes, n_points, coords_row_stride, B, D, H, W, rank,
@@ -4322,22 +4349,38 @@ static int op_forward_impl(const void *feats, int32_t dtype, int64_t feats_row_s
   rep.meta = meta;
   rep.dst = report_dev;
   return forward_impl(feats, dtype, feats_row_stride, C, n_points, keys, cstart, cend, meta, B, D,
-                      hw, int64_t(C) * D * hw, int64_t(D) * hw, hw, out, ws + L.scratch,
+                      hw, int64_t(C) * D * hw, int64_t(D) * hw, hw, out, sc + S.rows,
                       size_t(cells) * size_t(C) * sizeof(float), stream, rep);
+}
+
+size_t bevpool_op_index_bytes(int64_t n_points, int64_t n_cells) {
+  if (n_points < 0 || n_cells < 0) return 0;
+  return op_index_layout(n_points, n_cells).total;
+}
+
+size_t bevpool_op_scratch_bytes(int64_t n_points, int64_t n_cells, int32_t C) {
+  if (n_points < 0 || n_cells < 0 || C < 0) return 0;
+  return op_scratch_layout(n_points, n_cells, C).total;
+}
+
+size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C) {
+  if (n_points < 0 || n_cells < 0 || C < 0) return 0;
+  return op_index_layout(n_points, n_cells).total + op_scratch_layout(n_points, n_cells, C).total;
 }
 
 int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
                        const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
                        int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W, void *out,
-                       void *workspace, size_t workspace_bytes, int32_t *report, void *stream) {
+                       void *index, size_t index_bytes, void *scratch, size_t scratch_bytes,
+                       int32_t *report, void *stream) {
   g_last_error.clear();
   int32_t *report_dev = nullptr;
   if (report) {
     if (int st = report_address(report, &report_dev)) return st;
   }
   return op_forward_impl(feats, dtype, feats_row_stride, C, coords, coord_bytes,
-                         coords_row_stride, n_points, B, D, H, W, out, workspace,
-                         workspace_bytes, report_dev, stream);
+                         coords_row_stride, n_points, B, D, H, W, out, index, index_bytes,
+                         scratch, scratch_bytes, report_dev, stream);
 }
 
 int bevpool_op_forward_noalloc(const void *feats, int32_t dtype, int64_t feats_row_stride,
@@ -4345,24 +4388,23 @@ int bevpool_op_forward_noalloc(const void *feats, int32_t dtype, int64_t feats_r
                                int64_t coords_row_stride, int64_t n_points, int32_t B, int32_t D,
                                int32_t H, int32_t W, void *out, void *stream) {
   g_last_error.clear();
-  if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
-  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
-  if (n_points < 0 || n_points > int64_t(INT32_MAX))
-    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range", (long long)n_points);
+  if (int st = op_check_sizes(n_points, B, D, H, W, C)) return st;
   const int64_t cells = int64_t(B) * D * H * W;
-  if (cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "B*D*H*W exceeds 2^31-1");
-  const size_t need = op_layout(n_points, cells, C).total;
+  const size_t index_bytes = op_index_layout(n_points, cells).total;
+  const size_t need = index_bytes + op_scratch_layout(n_points, cells, C).total;
   if (need > kNoAllocScratchBytes)
     return fail(BEVPOOL_ESPACE,
                 "the allocation-free forward needs %zu bytes of scratch for n_points=%lld, "
                 "B*D*H*W=%lld, C=%d; its static scratch holds %zu (use bevpool_op_forward)",
                 need, (long long)n_points, (long long)cells, C, kNoAllocScratchBytes);
-  void *ws = noalloc_scratch();
+  char *ws = static_cast<char *>(noalloc_scratch());
   if (!ws) return BEVPOOL_EHIP;
   g_no_alloc_call = true;
+  // index first (index_bytes is a multiple of 256), then the call's scratch
   const int st = op_forward_impl(feats, dtype, feats_row_stride, C, coords, coord_bytes,
-                                 coords_row_stride, n_points, B, D, H, W, out, ws,
-                                 kNoAllocScratchBytes, nullptr, stream);
+                                 coords_row_stride, n_points, B, D, H, W, out, ws, index_bytes,
+                                 ws + index_bytes, kNoAllocScratchBytes - index_bytes, nullptr,
+                                 stream);
   g_no_alloc_call = false;
   return st;
 }
@@ -4371,25 +4413,22 @@ int bevpool_op_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                         int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
                         int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W,
                         void *x_grad, int64_t x_grad_row_stride, int32_t zero_dropped,
-                        void *workspace, size_t workspace_bytes, void *stream) {
+                        const void *index, size_t index_bytes, void *scratch,
+                        size_t scratch_bytes, void *stream) {
   g_last_error.clear();
-  if (B < 1 || D < 1 || H < 1 || W < 1) return fail(BEVPOOL_EINVAL, "B, D, H, W must be positive");
-  if (C < 1) return fail(BEVPOOL_EINVAL, "C must be positive");
-  if (n_points < 0 || n_points > int64_t(INT32_MAX))
-    return fail(BEVPOOL_EINVAL, "n_points=%lld out of range", (long long)n_points);
+  if (int st = op_check_sizes(n_points, B, D, H, W, C)) return st;
   const int64_t cells = int64_t(B) * D * H * W;
-  if (cells > int64_t(INT32_MAX)) return fail(BEVPOOL_EINVAL, "B*D*H*W exceeds 2^31-1");
-  if (!workspace) return fail(BEVPOOL_EINVAL, "null workspace");
-  const OpLayout L = op_layout(n_points, cells, C);
-  if (workspace_bytes < L.total)
-    return fail(BEVPOOL_ESPACE, "op workspace %zu bytes < required %zu", workspace_bytes, L.total);
-  char *ws = static_cast<char *>(workspace);
+  if (!index) return fail(BEVPOOL_EINVAL, "null index buffer");
+  const OpIndexLayout L = op_index_layout(n_points, cells);
+  if (index_bytes < L.total)
+    return fail(BEVPOOL_ESPACE, "op index buffer %zu bytes < required %zu", index_bytes, L.total);
+  const char *ix = static_cast<const char *>(index);
   return bevpool_backward(grad, dtype, grad_stride_b, grad_stride_c, grad_stride_z, C,
-                          reinterpret_cast<const int32_t *>(ws + L.rank), n_points,
-                          reinterpret_cast<const int32_t *>(ws + L.cstart),
-                          reinterpret_cast<const int32_t *>(ws + L.cend), B, D, int64_t(H) * W,
-                          x_grad, x_grad_row_stride, zero_dropped, ws + L.scratch,
-                          size_t(cells) * size_t(C) * dtype_size(dtype), stream);
+                          reinterpret_cast<const int32_t *>(ix + L.rank), n_points,
+                          reinterpret_cast<const int32_t *>(ix + L.cstart),
+                          reinterpret_cast<const int32_t *>(ix + L.cend), B, D, int64_t(H) * W,
+                          x_grad, x_grad_row_stride, zero_dropped, scratch, scratch_bytes,
+                          stream);
 }
 
 int bevpool_timing_enable(int enable) {

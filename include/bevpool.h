@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define BEVPOOL_ABI_VERSION 3
+#define BEVPOOL_ABI_VERSION 4
 
 /* status codes */
 #define BEVPOOL_OK 0
@@ -358,12 +358,17 @@ int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t gra
 /*
  * One-call op level: ops/bev_pool/src/bev_pool_triton.py:219-227
  * (bev_pool(feats, coords, B, D, H, W)) as bevpool_coord_ranks ->
- * bevpool_sort -> bevpool_forward on one caller-owned workspace, which keeps
- * the index (ranks, sorted keys, cell ranges) for bevpool_op_backward.
- * The workspace starts with the BEVPOOL_META_LEN int32 meta counters
- * (meta[BEVPOOL_META_N_BAD] = points whose rank falls outside [0, B*D*H*W):
- * they are excluded, where the reference CPU fallback raises).  One
- * workspace serves one forward/backward pair at a time.
+ * bevpool_sort -> bevpool_forward.  Two caller-owned buffers:
+ *   index    >= bevpool_op_index_bytes(n_points, B*D*H*W): what the backward
+ *            needs (meta counters, ranks, sorted keys, cell ranges); it
+ *            starts with the BEVPOOL_META_LEN int32 meta counters
+ *            (meta[BEVPOOL_META_N_BAD] = points whose rank falls outside
+ *            [0, B*D*H*W): they are excluded, where the reference CPU
+ *            fallback raises).  Keep it from the forward to its backward.
+ *   scratch  >= bevpool_op_scratch_bytes(n_points, B*D*H*W, C): the
+ *            index-stage workspace and the cell rows, needed only during
+ *            the call (free or reuse it afterwards).
+ * One index buffer serves one forward/backward pair at a time.
  *
  *   feats        dtype [n_points, C], row stride feats_row_stride, channel stride 1
  *   coords       int32 / int64 (coord_bytes 4 / 8) [n_points, 4] (x, y, z, b)
@@ -374,27 +379,42 @@ int bevpool_backward_depth(const float *grad, int64_t grad_stride_b, int64_t gra
  *                written by the call's last kernel (as bevpool_meta_report,
  *                folded in: no launch of its own): a host that cleared the
  *                flag polls it and then reads the count of excluded points
+ * bevpool_op_workspace_bytes is the sum of the two (the allocation-free
+ * forward below keeps both in one static array).
  */
+size_t bevpool_op_index_bytes(int64_t n_points, int64_t n_cells);
+size_t bevpool_op_scratch_bytes(int64_t n_points, int64_t n_cells, int32_t C);
 size_t bevpool_op_workspace_bytes(int64_t n_points, int64_t n_cells, int32_t C);
 
 int bevpool_op_forward(const void *feats, int32_t dtype, int64_t feats_row_stride, int32_t C,
                        const void *coords, int32_t coord_bytes, int64_t coords_row_stride,
                        int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W, void *out,
-                       void *workspace, size_t workspace_bytes, int32_t *report, void *stream);
+                       void *index, size_t index_bytes, void *scratch, size_t scratch_bytes,
+                       int32_t *report, void *stream);
 
 /*
  * bevpool_op_forward without a workspace argument, for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid allocation).  No counterpart in the
- * reference.  The workspace lives in a static device array of
- * BEVPOOL_NOALLOC_MAX_BYTES bytes inside the library, one per GPU, held until
- * the process ends; a call whose workspace (bevpool_op_workspace_bytes)
- * exceeds it returns BEVPOOL_ESPACE.  The call allocates nothing (no
- * hipMalloc, no events even with timing enabled).  Every call on one GPU
- * uses that GPU's array, which keeps the last call's contents: calls that
- * overlap on one GPU (concurrent streams or threads) race, and the index
- * left behind is not kept for a backward.  Points with invalid coords are
- * excluded, as in bevpool_op_forward; the count is not reported.
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference.  The workspace lives in a
+ * static device array of BEVPOOL_NOALLOC_MAX_BYTES bytes inside the
+ * library's code object, one copy per GPU: every GPU on which any entry
+ * point of this library has run holds its 96 MiB until the process ends,
+ * whether or not this entry point is used.  A call whose workspace
+ * (bevpool_op_workspace_bytes) exceeds it returns BEVPOOL_ESPACE.
+ *
+ * The first call on a device resolves the array's device address
+ * (hipGetSymbolAddress, cached per device); if no kernel of the library has
+ * run on that device yet, that lookup loads the code object there, which
+ * reserves the array.  Make one call (or any other library call) on each
+ * device before relying on the no-allocation property.  After that a call
+ * allocates nothing: no hipMalloc, no events even with timing enabled.
+ * Graph capture of this entry point is not tested and not claimed.
+ *
+ * Every call on one GPU uses that GPU's array, which keeps the last call's
+ * contents: calls that overlap on one GPU (concurrent streams or threads)
+ * race, and the index left behind is not kept for a backward.  Points with
+ * invalid coords are excluded, as in bevpool_op_forward; the count is not
+ * reported.
  */
 #define BEVPOOL_NOALLOC_MAX_BYTES ((size_t)96 << 20)
 
@@ -405,16 +425,18 @@ int bevpool_op_forward_noalloc(const void *feats, int32_t dtype, int64_t feats_r
 
 /*
  * Backward of bevpool_op_forward (bev_pool_triton.py:189-216): x_grad[p, :]
- * = grad at p's cell, on the index the last bevpool_op_forward left in the
- * workspace.  grad element (b, c, z, xy) at b*grad_stride_b + c*grad_stride_c
- * + z*grad_stride_z + xy (xy = x*W + y contiguous); zero_dropped as
- * bevpool_backward.
+ * = grad at p's cell, on the index the forward left in `index`.  grad
+ * element (b, c, z, xy) at b*grad_stride_b + c*grad_stride_c +
+ * z*grad_stride_z + xy (xy = x*W + y contiguous); zero_dropped as
+ * bevpool_backward.  scratch >= bevpool_backward_scratch_bytes(B*D*H*W, C,
+ * dtype) (bevpool_op_scratch_bytes is always enough).
  */
 int bevpool_op_backward(const void *grad, int32_t dtype, int64_t grad_stride_b,
                         int64_t grad_stride_c, int64_t grad_stride_z, int32_t C,
                         int64_t n_points, int32_t B, int32_t D, int32_t H, int32_t W,
                         void *x_grad, int64_t x_grad_row_stride, int32_t zero_dropped,
-                        void *workspace, size_t workspace_bytes, void *stream);
+                        const void *index, size_t index_bytes, void *scratch,
+                        size_t scratch_bytes, void *stream);
 
 /*
  * Legacy native interface: the reference's pybind extension functions

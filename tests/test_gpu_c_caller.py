@@ -57,12 +57,15 @@ int main(void) {
   float *rows = malloc(cells * C * sizeof(float));
   oracle_forward(feats, C, C, rank, N, cells, rows);
 
-  const size_t ws_bytes = bevpool_op_workspace_bytes(N, cells, C);
-  void *d_feats, *d_coords, *d_out, *d_ws, *d_grad, *d_xg;
+  const size_t ix_bytes = bevpool_op_index_bytes(N, cells);
+  const size_t sc_bytes = bevpool_op_scratch_bytes(N, cells, C);
+  CHECK(bevpool_op_workspace_bytes(N, cells, C) == ix_bytes + sc_bytes);
+  void *d_feats, *d_coords, *d_out, *d_ix, *d_sc, *d_grad, *d_xg;
   CHECK(hipMalloc(&d_feats, N * C * 4) == hipSuccess);
   CHECK(hipMalloc(&d_coords, N * 16) == hipSuccess);
   CHECK(hipMalloc(&d_out, cells * C * 4) == hipSuccess);
-  CHECK(hipMalloc(&d_ws, ws_bytes) == hipSuccess);
+  CHECK(hipMalloc(&d_ix, ix_bytes) == hipSuccess);
+  CHECK(hipMalloc(&d_sc, sc_bytes) == hipSuccess);
   CHECK(hipMalloc(&d_grad, cells * C * 4) == hipSuccess);
   CHECK(hipMalloc(&d_xg, N * C * 4) == hipSuccess);
   CHECK(hipMemcpy(d_feats, feats, N * C * 4, hipMemcpyHostToDevice) == hipSuccess);
@@ -70,15 +73,15 @@ int main(void) {
 
   /* forward: (B, C, D, H, W) contiguous */
   int st = bevpool_op_forward(d_feats, BEVPOOL_F32, C, (int32_t)C, d_coords, 4, 4, N,
-                              (int32_t)B, (int32_t)D, (int32_t)H, (int32_t)W, d_out, d_ws,
-                              ws_bytes, NULL, NULL);
+                              (int32_t)B, (int32_t)D, (int32_t)H, (int32_t)W, d_out, d_ix,
+                              ix_bytes, d_sc, sc_bytes, NULL, NULL);
   if (st) printf("op_forward: %s\n", bevpool_last_error());
   CHECK(st == BEVPOOL_OK);
   CHECK(hipDeviceSynchronize() == hipSuccess);
   float *out = malloc(cells * C * 4);
   int32_t meta[BEVPOOL_META_LEN];
   CHECK(hipMemcpy(out, d_out, cells * C * 4, hipMemcpyDeviceToHost) == hipSuccess);
-  CHECK(hipMemcpy(meta, d_ws, sizeof(meta), hipMemcpyDeviceToHost) == hipSuccess);
+  CHECK(hipMemcpy(meta, d_ix, sizeof(meta), hipMemcpyDeviceToHost) == hipSuccess);
   CHECK(meta[BEVPOOL_META_N_KEPT] == N - nbad_exp);
   CHECK(meta[BEVPOOL_META_N_BAD] == nbad_exp);
   CHECK(meta[BEVPOOL_META_FIRST_BAD] == first_bad);
@@ -102,9 +105,16 @@ int main(void) {
       for (int64_t s = 0; s < D * H * W; ++s)
         grad_rows[(b * D * H * W + s) * C + c] = grad[b * per_b + c * per_c + s];
   CHECK(hipMemcpy(d_grad, grad, cells * C * 4, hipMemcpyHostToDevice) == hipSuccess);
+  /* the forward's scratch is not needed any more: the backward gets a fresh
+     one, filled with junk first */
+  CHECK(hipFree(d_sc) == hipSuccess);
+  const size_t bsc_bytes = bevpool_backward_scratch_bytes(cells, (int32_t)C, BEVPOOL_F32);
+  CHECK(bsc_bytes <= sc_bytes);
+  CHECK(hipMalloc(&d_sc, bsc_bytes) == hipSuccess);
+  CHECK(hipMemset(d_sc, 0x5a, bsc_bytes) == hipSuccess);
   st = bevpool_op_backward(d_grad, BEVPOOL_F32, per_b, per_c, H * W, (int32_t)C, N,
-                           (int32_t)B, (int32_t)D, (int32_t)H, (int32_t)W, d_xg, C, 1, d_ws,
-                           ws_bytes, NULL);
+                           (int32_t)B, (int32_t)D, (int32_t)H, (int32_t)W, d_xg, C, 1, d_ix,
+                           ix_bytes, d_sc, bsc_bytes, NULL);
   if (st) printf("op_backward: %s\n", bevpool_last_error());
   CHECK(st == BEVPOOL_OK);
   CHECK(hipDeviceSynchronize() == hipSuccess);

@@ -407,20 +407,22 @@ def test_op_entry_zero_dropped_flag(pkg, cuda):
     keep = torch.ones(5000, dtype=torch.bool)
     keep[[3, 77, 4999]] = False
     f, c = feats.to(cuda), coords.to(cuda)
-    ws = P.op_workspace(5000, 2 * 12 * 13, 20, cuda)
+    index = P.op_index(5000, 2 * 12 * 13, cuda)
+    scratch = P.op_scratch(5000, 2 * 12 * 13, 20, cuda)
     out = torch.empty((2, 20, 1, 12, 13), device=cuda)
-    P.op_forward(f, c, *sizes, out, ws)
+    P.op_forward(f, c, *sizes, out, index, scratch)
+    scratch.fill_(0x5a)  # the backward needs only the index the forward left
     assert_bit_equal(out, ref.bev_pool(feats[keep], coords[keep], *sizes), 'op entry forward')
-    meta = P.op_meta(ws).cpu()
+    meta = P.op_meta(index).cpu()
     assert int(meta[L.META_N_BAD]) == 3 and int(meta[L.META_FIRST_BAD]) == 3
     g = torch.randn(out.shape, generator=torch.Generator().manual_seed(22)).to(cuda)
     exp = torch.zeros(5000, 20)
     exp[keep] = ref.backward_gather(g.cpu(), coords[keep], *sizes)
     xg = torch.full((5000, 20), 7.0, device=cuda)
-    P.op_backward(g, 20, 5000, *sizes, xg, ws, zero_dropped=True)
+    P.op_backward(g, 20, 5000, *sizes, xg, index, scratch, zero_dropped=True)
     assert_bit_equal(xg, exp, 'zero_dropped = 1')
     xg = torch.full((5000, 20), 7.0, device=cuda)
-    P.op_backward(g, 20, 5000, *sizes, xg, ws, zero_dropped=False)
+    P.op_backward(g, 20, 5000, *sizes, xg, index, scratch, zero_dropped=False)
     exp[~keep] = 7.0
     assert_bit_equal(xg, exp, 'zero_dropped = 0')
 

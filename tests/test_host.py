@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(pkg):
     lib = pkg.library()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.bevpool_abi_version() == 3
+    assert lib.bevpool_abi_version() == 4
     assert lib.bevpool_last_error() == b''
 
 
@@ -150,6 +150,33 @@ def test_no_cpu_fallback(pkg):
         pkg.lss_bev_pool(geom, x, *pkg.gen_dx_bx((-1, 1, 1), (-1, 1, 1), (-1, 1, 2)))
 
 
+def test_binding_keeps_cpu_branch(pkg):
+    """The op-level binding of INTEGRATION.md replaces only the GPU branch of
+    ``bev_pool_triton.py:219-227``: CPU tensors still reach the reference's
+    CPU fallback (restated in oracle/ for this test) and give the reference's
+    known answer (``tests/test_ops/test_bev_pool.py:57-84``); calling this
+    package directly with CPU tensors raises the documented error."""
+    from oracle import torch_fallback as ref
+
+    def bev_pool(feats, coords, B, D, H, W):  # the binding, as INTEGRATION.md writes it
+        ref.check_inputs(feats, coords, B, D, H, W)
+        if feats.is_cuda:
+            return pkg.bev_pool(feats, coords, B, D, H, W)
+        out = ref.bev_pool_cpu(feats, coords, B, D, H, W)
+        return out.permute(0, 4, 1, 2, 3).contiguous()
+
+    k = json.loads((GOLDEN / 'known_case.json').read_text())
+    feats = torch.tensor(k['feats'], requires_grad=True)
+    coords = torch.tensor(k['coords'], dtype=torch.int32)
+    out = bev_pool(feats, coords, k['B'], k['D'], k['H'], k['W'])
+    assert out.is_contiguous() and list(out.shape) == k['expected_shape']
+    assert torch.equal(out.detach(), torch.tensor(k['expected']))
+    out.sum().backward()
+    assert torch.equal(feats.grad, torch.ones(3, 2))
+    with pytest.raises(RuntimeError, match='runs the bev_pool path on a ROCm GPU only'):
+        pkg.bev_pool(feats.detach(), coords, k['B'], k['D'], k['H'], k['W'])
+
+
 def test_gen_dx_bx_matches_reference_restatement(pkg):
     from oracle import torch_fallback as ref
 
@@ -255,13 +282,23 @@ def test_op_and_legacy_status_codes(pkg):
     lib = pkg.library()
     ws = np.zeros(1 << 12, np.uint8)
     need = lib.bevpool_op_workspace_bytes(1000, 100, 8)
-    assert need > 1000 * 12 + 100 * 8 * 4 and need % 256 == 0
+    ix = lib.bevpool_op_index_bytes(1000, 100)
+    sc = lib.bevpool_op_scratch_bytes(1000, 100, 8)
+    assert need == ix + sc and ix % 256 == 0 and sc % 256 == 0
+    assert ix >= 1000 * 12 + 100 * 8 and sc >= 100 * 8 * 4
     st = lib.bevpool_op_forward(None, 0, 8, 8, None, 4, 4, 1000, 1, 1, 10, 10, None,
-                                ws.ctypes.data, ws.size, None, None)
-    assert st == -3 and b'op workspace' in lib.bevpool_last_error()
+                                ws.ctypes.data, ws.size, ws.ctypes.data, ws.size, None, None)
+    assert st == -3 and b'op index buffer' in lib.bevpool_last_error()
+    big = np.zeros(ix, np.uint8)
+    st = lib.bevpool_op_forward(None, 0, 8, 8, None, 4, 4, 1000, 1, 1, 10, 10, None,
+                                big.ctypes.data, big.size, ws.ctypes.data, 256, None, None)
+    assert st == -3 and b'op scratch' in lib.bevpool_last_error()
     st = lib.bevpool_op_forward(None, 0, 8, 8, None, 4, 4, 10, 1, 0, 10, 10, None,
-                                ws.ctypes.data, ws.size, None, None)
+                                ws.ctypes.data, ws.size, ws.ctypes.data, ws.size, None, None)
     assert st == -1
+    st = lib.bevpool_op_backward(None, 0, 1, 1, 1, 8, 1000, 1, 1, 10, 10, None, 8, 1,
+                                 ws.ctypes.data, 256, ws.ctypes.data, ws.size, None)
+    assert st == -3 and b'op index buffer' in lib.bevpool_last_error()
     st = lib.bevpool_legacy_forward(None, 10, 0, None, None, None, 0, None, 1, 1, 1, 1,
                                     ws.ctypes.data, None, None)
     assert st == -1 and b'C must be positive' in lib.bevpool_last_error()

@@ -2,8 +2,9 @@
 workspace is a static device array inside the library) through the C ABI,
 against ``bevpool_op_forward`` with a caller-owned workspace on the same
 inputs: bit-exact on two calls in a row, the second with a smaller input (the
-array keeps the first call's contents), and the documented refusal of a
-workspace larger than the array."""
+array keeps the first call's contents), the documented refusal of a
+workspace larger than the array, and, after a warm-up call, no change in free
+device memory and no timing records."""
 from __future__ import annotations
 
 import ctypes
@@ -34,9 +35,10 @@ def _with_workspace(feats, coords, sizes):
 
     B, D, H, W = sizes
     n, C = feats.shape
-    ws = P.op_workspace(n, B * D * H * W, C, feats.device)
+    index = P.op_index(n, B * D * H * W, feats.device)
+    scratch = P.op_scratch(n, B * D * H * W, C, feats.device)
     out = torch.empty((B, C, D, H, W), dtype=feats.dtype, device=feats.device)
-    P.op_forward(feats, coords, B, D, H, W, out, ws)
+    P.op_forward(feats, coords, B, D, H, W, out, index, scratch)
     return out
 
 
@@ -79,3 +81,30 @@ def test_noalloc_refuses_oversized(pkg, cuda):
     out = torch.empty((1, 8, 1, 10, 10), device=cuda)
     assert _noalloc(pkg, f.to(cuda), c.to(cuda), (1, 1, 10, 10), out) == 0
     assert_bit_equal(out, ref.bev_pool(f, c, 1, 1, 10, 10), 'after refusal')
+
+
+def test_noalloc_allocates_nothing(pkg, cuda):
+    """The property the entry point exists for: after one warm-up call on the
+    device, a call leaves the device's free memory unchanged (no hipMalloc)
+    and records no timing events even with the library's timing on."""
+    from bevfusion_triton_amd import _lib as L
+
+    sizes = (1, 2, 40, 50)
+    f, c = rand_case(30000, 24, *sizes, seed=6)
+    f, c = f.to(cuda), c.to(cuda)
+    out = torch.empty((1, 24, 2, 40, 50), device=cuda)
+    assert _noalloc(pkg, f, c, sizes, out) == 0  # warm-up: resolves the array's address
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info(cuda)
+    L.timing_reset()
+    L.timing_enable(True)
+    try:
+        for _ in range(3):
+            assert _noalloc(pkg, f, c, sizes, out) == 0, pkg.library().bevpool_last_error()
+        torch.cuda.synchronize()
+    finally:
+        L.timing_enable(False)
+    free1, _ = torch.cuda.mem_get_info(cuda)
+    assert free1 == free0, f'free device memory changed by {free0 - free1} bytes'
+    assert L.timing_read() == {}, 'the allocation-free call recorded timing events'
+    assert_bit_equal(out, ref.bev_pool(f.cpu(), c.cpu(), *sizes), 'noalloc after warm-up')
