@@ -491,9 +491,11 @@ def main():
 
 
 def config_figure(pkg, lib, name, dev):
-    """fwd / bwd of one benchmark configuration: median of 20 back-to-back
-    steps by HIP events after 40 warm-ups, the accumulation kernel's average
-    by the library's launch events, and the path's algorithmic bandwidth.
+    """One benchmark configuration after 40 untimed steps: the time of 20
+    back-to-back fwd+bwd steps (HIP events around the loop only; `step_us`,
+    the figure the path bandwidth uses), the median fwd and bwd halves of 20
+    more steps with events between the halves, and the per-kernel averages of
+    5 more steps with the library's launch events on.
     fp32 configurations run the vtransform-level call on the full frustum;
     bf16 runs the op-level bev_pool on the kept points (fp32 accumulation,
     bf16 output and gradient)."""
@@ -546,9 +548,17 @@ def config_figure(pkg, lib, name, dev):
         fwd_b = s * C * n_kept + s * C * cells
         bwd_b = s * C * n_occ + s * C * n_kept
         level, n_step = 'op', n_kept
-    for _ in range(40):  # as the default run: ~10 ms of this load before timing
+    for _ in range(40):  # past the first steps' transient (~10 ms of this load)
         bwd(fwd())
     torch.cuda.synchronize()
+    # back-to-back steps, events only around the loop (as the headline's steps)
+    e_a, e_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e_a.record()
+    for _ in range(20):
+        bwd(fwd())
+    e_b.record()
+    torch.cuda.synchronize()
+    step_ms = e_a.elapsed_time(e_b) / 20
     evs = []
     for _ in range(20):
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
@@ -575,10 +585,13 @@ def config_figure(pkg, lib, name, dev):
     return {
         'config': name, 'level': level, 'dtype': str(spec.dtype).replace('torch.', ''),
         'batch': B, 'bev': [X, Y, Z], 'frustum_points': n_all, 'n_kept': n_kept,
-        'n_occ': n_occ, 'fwd_us': round(t_fwd * 1e3, 1), 'bwd_us': round(t_bwd * 1e3, 1),
-        'points_per_s': round(n_step / t, 1),
+        'n_occ': n_occ, 'step_us': round(step_ms * 1e3, 1),
+        'fwd_us': round(t_fwd * 1e3, 1), 'bwd_us': round(t_bwd * 1e3, 1),
+        'points_per_s': round(n_step / (step_ms * 1e-3), 1),
         'path_alg_MB': round((fwd_b + bwd_b) / 1e6, 1),
-        'path_achieved_GBps': round((fwd_b + bwd_b) / t / 1e9, 1),
+        'path_achieved_GBps': round((fwd_b + bwd_b) / (step_ms * 1e-3) / 1e9, 1),
+        'path_frac_of_peak': round((fwd_b + bwd_b) / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        'split_path_achieved_GBps': round((fwd_b + bwd_b) / t / 1e9, 1),
         'accum_rows_us': round(acc_us, 1) if acc_us else None,
         'accum_rows_GBps': round(acc_b / (acc_us * 1e-6) / 1e9, 1) if acc_us else None,
         'kernels_us_per_step': {k: round(v, 1) for k, v in sorted(kt.items())},
