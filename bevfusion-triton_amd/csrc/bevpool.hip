@@ -1746,7 +1746,6 @@ __device__ __forceinline__ void loader_step(LoaderRing<kSlots> &R, int lt,
                                             u32x4 *__restrict__ buf0, u32x4 *__restrict__ buf1,
                                             int *__restrict__ rk0s, int *__restrict__ rk1s,
                                             const DepthRows &dr) {
-  constexpr bool kMul = kRows == kRowsDepth;
   ring_rows<kSlots, r, kRows>(R, lt, kw, xb, ld_bytes, col_bytes, pr, k + kDepth, dr);
   ring_index<kSlots, r, kRows>(R, lt, kw, pr, k + 2 * kDepth);
   if (k + 1 < nst) {
@@ -1895,7 +1894,6 @@ __global__ __launch_bounds__(kPipeThreads) void accum_pipe_kernel(
     const char *__restrict__ xb, int64_t ld_bytes, int C, int CB,
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ meta,
     const int32_t *__restrict__ cend, float *__restrict__ acc, int64_t P, DepthRows dr) {
-  constexpr bool kMul = kRows == kRowsDepth;
   using raw = typename T::raw;
   extern __shared__ u32x4 smem4[];
   const int rowq_max = CB * int(sizeof(raw)) / 16;
