@@ -3074,6 +3074,13 @@ DigitPlan plan_digits(int64_t n_cells) {
   DigitPlan p;
   if (BEVPOOL_BUCKET_SORT && total_bits > kMaxDigitBits && total_bits <= 2 * kMaxDigitBits) {
     p.bits[0] = (total_bits + 1) / 2;  // high digit: global pass
+    // Narrower groups shorten the per-group sort, whose largest group sets
+    // its length; tile histograms of up to 2^9 digits cost the global pass
+    // no more than 2^8, 2^10 cost it ~5 us at 1 x 360 x 360 (MI355X).  So a
+    // 16-bit rank space takes 9 + 7 bits (256 x 256: per-group sort 25.0 ->
+    // 16.9 us), while 17 bits keep 9 + 8.
+    if (total_bits - p.bits[0] > 7 && p.bits[0] < 9)
+      p.bits[0] = total_bits - 7 < 9 ? total_bits - 7 : 9;
     p.local_bits = total_bits - p.bits[0];
     p.shift[0] = p.local_bits;
     return p;

@@ -184,16 +184,18 @@ def test_half_channel_blocks(pkg, cuda, dtype, C):
 
 @pytest.mark.parametrize('name,sizes', [
     ('11-bit ranks, 2-cell groups', (1, 1, 5, 205)),
+    ('16-bit ranks, 9 + 7 bits', (1, 1, 256, 256)),
+    ('16-bit ranks, 9 + 7 bits, one group holding most points', (1, 1, 256, 256)),
     ('20-bit ranks, 1024-cell groups', (1, 1, 1024, 1024)),
     ('17-bit ranks, one group holding most points', (1, 1, 360, 360)),
     ('20-bit ranks, one group holding most points', (1, 1, 1024, 1024)),
     ('20-bit ranks, groups at slice boundaries', (1, 1, 1024, 1024)),
 ])
 def test_bucket_sort_edges(pkg, cuda, name, sizes):
-    """Ranks of 11..20 bits: one global pass by the high 10 bits, then the
-    low bits are sorted per group (one block per group of up to 512 cells;
-    groups of 1024 cells are cut into slices of 8192 keys) and the group's
-    cell ranges written.  Cases: the smallest groups, the largest rank space,
+    """Ranks of 11..20 bits: one global pass by the high digit (half the
+    bits rounded up; 9 of 16), then the low bits are sorted per group (one
+    block per group of up to 512 cells; groups of 1024 cells are cut into
+    slices of 8192 keys) and the group's cell ranges written.  Cases: the smallest groups, the largest rank space,
     one group far larger than the rest (90% of the points in 3 cells, sizes
     not multiples of 64) with empty groups around it, and groups of exactly
     1, 2 and 4 slices and one key more."""
