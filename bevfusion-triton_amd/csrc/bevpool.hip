@@ -999,42 +999,49 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
 
 // Second half of the sort when the ranks need 11..20 bits.  One global pass
 // (radix_scatter_kernel<true> by the high digit rank >> lbits) has grouped
-// the kept keys by high digit, each group in point order.  Block b sorts
-// group b stably by the low lbits bits, so the keys end sorted by rank with
-// ties in point order, as two LSD passes would leave them, and writes the
-// dense [start, end) of the group's 2^lbits cells (0, 0 when empty), which
-// replaces cell_ranges_kernel and the zeroing of the cell ranges.
-// Wave w of kBucketWaves owns the w-th slice of the group (a multiple of 64
+// the kept keys by high digit, each group in point order.  The keys of group
+// b are sorted stably by the low lbits bits, so the keys end sorted by rank
+// with ties in point order, as two LSD passes would leave them, and the dense
+// [start, end) of the group's 2^lbits cells is written (0, 0 when empty),
+// which replaces cell_ranges_kernel and the zeroing of the cell ranges.
+// A group of gn keys is cut into P = min(parts_max, ceil(gn / part_keys))
+// consecutive parts, one block each, so that a large group (the cells near
+// the cameras) is not ranked by one block alone.  The block of part p first
+// counts the digits of the group's other keys (those before its part apart),
+// then walks its own part as one block walks a whole group:
+// Wave w of kBucketWaves owns the w-th slice of the part (a multiple of 64
 // keys) and walks it 64 keys at a time, in order, twice: the first walk
 // counts its digits, the second puts each key at
 //   (group start) + (smaller digits in the group) + (same digit in earlier
-//   waves) + (same digit earlier in this wave),
+//   parts) + (same digit in earlier waves) + (same digit earlier in this
+//   wave),
 // the last term from a ballot-built peer mask as in radix_scatter_kernel.
-// Keys are loaded kBucketBatch sub-batches (of 64) at a time; a wave whose slice
-// fits in one batch keeps it in registers for the second walk.  Otherwise
-// the second walk drains each batch's loads before its first key store:
-// vmcnt counts loads and stores together, so a wait for a load issued after
-// a store would also wait for the store.  Dynamic LDS:
-// kBucketWaves * 2^lbits ints (16 waves, up to 512 digits: at most 32 KB per
-// block).  Groups of 1024 cells take the sliced form below instead.
-
+// No block waits for another.  Block i takes part parts_max - 1 - i / n of
+// group i % n (n groups): the blocks of the later parts, of which only the
+// large groups' do any work, come first, so that those start at once.  The
+// block of part 0 writes the cell ranges.  Keys are loaded kBucketBatch
+// sub-batches (of 64) at a time; a wave whose slice fits in one batch keeps
+// it in registers for the second walk.  Otherwise the second walk drains
+// each batch's loads before its first key store: vmcnt counts loads and
+// stores together, so a wait for a load issued after a store would also wait
+// for the store.  Dynamic LDS: (kBucketWaves + 2) * 2^lbits ints (16 waves,
+// up to 512 digits: at most 36 KB per block).  Groups of 1024 cells take the
+// sliced form below instead.
 template <int kBucketWaves>
 __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
     const uint64_t *__restrict__ keys_in, const int32_t *__restrict__ totals,
     const int32_t *__restrict__ gstart, int n_buckets, int64_t n_cells,
     uint64_t *__restrict__ keys_out, int32_t *__restrict__ cstart, int32_t *__restrict__ cend,
-    int lbits) {
+    int lbits, int parts_max, int part_keys) {
   constexpr int kBucketThreads = 64 * kBucketWaves;
   // sub-batches per load batch: 12 keeps the 16-wave kernel within 64 VGPRs
   // (56; two blocks per CU) and a wave's part of any group up to 12,288 keys
   // in registers between its two walks (16 spills)
   constexpr int kBucketBatch = 12;
-  extern __shared__ int s_cnt[];  // [kBucketWaves][R]
+  extern __shared__ int s_cnt[];  // [kBucketWaves][R] own part, then [R] other parts, [R] before
   __shared__ int s_scan[kBucketWaves];
-  // block i takes group i: the large groups (cells near the cameras) are
-  // consecutive, and round-robin blocks spread them over the XCDs
-  const int bkt = int(blockIdx.x);
-  if (bkt >= n_buckets) return;
+  const int bkt = int(blockIdx.x) % n_buckets;
+  const int part = parts_max - 1 - int(blockIdx.x) / n_buckets;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const int R = 1 << lbits;
   const unsigned mask = unsigned(R - 1);
@@ -1042,15 +1049,51 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
   // group start (keys of smaller high digits, from the global pass) and size
   const int gs = gstart[bkt];
   const int gn = totals[bkt];
-  for (int d = tid; d < kBucketWaves * R; d += kBucketThreads) s_cnt[d] = 0;
-  const int64_t q = (int64_t(gn) + kBucketThreads - 1) / kBucketThreads * 64;  // keys per wave
+  const int np = gn > part_keys ? (gn + part_keys - 1) / part_keys : 1;
+  const int P = np < parts_max ? np : parts_max;
+  if (part >= P) return;
+  // this part: [ps, pe), a multiple of 64 keys but the last
+  const int L = ((gn + P - 1) / P + 63) & ~63;
   const int64_t ge = int64_t(gs) + gn;
-  const int wb = int(gs + w * q < ge ? gs + w * q : ge);
-  const int we = int(gs + (w + 1) * q < ge ? gs + (w + 1) * q : ge);
+  const int ps = int(gs + int64_t(part) * L < ge ? gs + int64_t(part) * L : ge);
+  const int pe = int(gs + int64_t(part + 1) * L < ge ? gs + int64_t(part + 1) * L : ge);
+  int *s_out = s_cnt + kBucketWaves * R;  // digits of the group's other parts
+  int *s_before = s_out + R;              // digits of the parts before this one
+  for (int d = tid; d < (kBucketWaves + 2) * R; d += kBucketThreads) s_cnt[d] = 0;
+  const int64_t q = (int64_t(pe - ps) + kBucketThreads - 1) / kBucketThreads * 64;  // keys per wave
+  const int wb = int(ps + w * q < pe ? ps + w * q : pe);
+  const int we = int(ps + (w + 1) * q < pe ? ps + (w + 1) * q : pe);
   __syncthreads();
 
-  int *cnt = s_cnt + w * R;
   uint64_t key[kBucketBatch];
+  if (P > 1) {
+    // the other parts' keys: [gs, ps) (counted as before this part too) and
+    // [pe, ge), each range cut into wave slices
+#pragma unroll 1
+    for (int r = 0; r < 2; ++r) {
+      const int a = r == 0 ? gs : pe, e = r == 0 ? ps : int(ge);
+      const int64_t qo = (int64_t(e - a) + kBucketThreads - 1) / kBucketThreads * 64;
+      const int ob = int(a + w * qo < e ? a + w * qo : e);
+      const int oe = int(a + (w + 1) * qo < e ? a + (w + 1) * qo : e);
+      for (int e0 = ob; e0 < oe; e0 += 64 * kBucketBatch) {
+#pragma unroll
+        for (int j = 0; j < kBucketBatch; ++j) {
+          const int i = e0 + 64 * j + lane;
+          if (e0 + 64 * j < oe) key[j] = keys_in[i < oe ? i : ob];
+        }
+#pragma unroll
+        for (int j = 0; j < kBucketBatch; ++j)
+          if (e0 + 64 * j < oe) {
+            const unsigned dg = key_digit(key[j], 0, mask);
+            const bool valid = e0 + 64 * j + lane < oe;
+            count_digit_runs(s_out, dg, valid);
+            if (r == 0) count_digit_runs(s_before, dg, valid);
+          }
+      }
+    }
+  }
+
+  int *cnt = s_cnt + w * R;
   const bool resident = we - wb <= 64 * kBucketBatch;  // wave-uniform
   for (int e0 = wb; e0 < we; e0 += 64 * kBucketBatch) {
     // sub-batches past the slice end are skipped (wave-uniform tests)
@@ -1067,16 +1110,18 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
   __syncthreads();
 
   // digit starts within the group (digits kPer * tid + i), the cells'
-  // ranges, per-wave bases
+  // ranges (part 0), per-wave bases of this part
   constexpr int kPer = kMaxRadix / kBucketThreads;  // digits per thread (1 or 2)
   int tot[kPer], tsum = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int d = kPer * tid + i;
     tot[i] = 0;
-    if (d < R)
+    if (d < R) {
 #pragma unroll
       for (int ww = 0; ww < kBucketWaves; ++ww) tot[i] += s_cnt[ww * R + d];
+      tot[i] += s_out[d];
+    }
     tsum += tot[i];
   }
   int gtotal;
@@ -1086,11 +1131,11 @@ __global__ __launch_bounds__(64 * kBucketWaves, 8) void bucket_sort_kernel(
     const int d = kPer * tid + i;
     if (d < R) {
       const int64_t cell = int64_t(bkt) * R + d;
-      if (cell < n_cells) {
+      if (part == 0 && cell < n_cells) {
         cstart[cell] = tot[i] ? ex : 0;
         cend[cell] = tot[i] ? ex + tot[i] : 0;
       }
-      int run = ex;
+      int run = ex + s_before[d];
 #pragma unroll
       for (int ww = 0; ww < kBucketWaves; ++ww) {
         const int c = s_cnt[ww * R + d];
@@ -3060,6 +3105,19 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 #ifndef BEVPOOL_BUCKET_SORT
 #define BEVPOOL_BUCKET_SORT 1
 #endif
+// Per-group sort: a group of more than kBucketPartKeys keys is ranked by up to
+// kBucketParts blocks.  Each part's block also counts the rest of its group,
+// so more parts cost more counting: at 1 x 360 x 360 the per-group sort took
+// 21.6 us with one block per group, 19.0 with 2 parts above 8192 keys, 20.0
+// with 4, 20.7 with 4 above 6144 keys and 22.6 with 4 above 4096 (MI355X).
+#ifndef BEVPOOL_BUCKET_PARTS
+#define BEVPOOL_BUCKET_PARTS 2
+#endif
+#ifndef BEVPOOL_BUCKET_PART_KEYS
+#define BEVPOOL_BUCKET_PART_KEYS 8192
+#endif
+constexpr int kBucketParts = BEVPOOL_BUCKET_PARTS;
+constexpr int kBucketPartKeys = BEVPOOL_BUCKET_PART_KEYS;
 struct DigitPlan {
   int passes = 1;
   int bits[4] = {1, 0, 0, 0};
@@ -3722,9 +3780,10 @@ static int sort_impl(const int32_t *rank, int64_t n_points, int64_t n_cells, uin
     // groups of at most 2^9 cells -> sorted keys and the dense cell ranges
     LaunchTimer t("bucket_sort", s);
     const int64_t n_buckets = ceil_div(n_cells, int64_t(1) << plan.local_bits);
-    hipLaunchKernelGGL(bucket_sort_kernel<16>, dim3(unsigned(n_buckets)), dim3(16 * 64),
-                       size_t(16) << plan.local_bits << 2, s, src, totals, gstart, int(n_buckets),
-                       n_cells, keys, cell_start, cell_end, plan.local_bits);
+    hipLaunchKernelGGL(bucket_sort_kernel<16>, dim3(unsigned(n_buckets * kBucketParts)),
+                       dim3(16 * 64), size_t(16 + 2) << plan.local_bits << 2, s, src, totals,
+                       gstart, int(n_buckets), n_cells, keys, cell_start, cell_end,
+                       plan.local_bits, kBucketParts, kBucketPartKeys);
     return check_launch("bucket_sort");
   }
   {

@@ -186,6 +186,7 @@ def test_half_channel_blocks(pkg, cuda, dtype, C):
     ('11-bit ranks, 2-cell groups', (1, 1, 5, 205)),
     ('16-bit ranks, 9 + 7 bits', (1, 1, 256, 256)),
     ('16-bit ranks, 9 + 7 bits, one group holding most points', (1, 1, 256, 256)),
+    ('17-bit ranks, groups at the part threshold', (1, 1, 360, 360)),
     ('20-bit ranks, 1024-cell groups', (1, 1, 1024, 1024)),
     ('17-bit ranks, one group holding most points', (1, 1, 360, 360)),
     ('20-bit ranks, one group holding most points', (1, 1, 1024, 1024)),
@@ -193,14 +194,35 @@ def test_half_channel_blocks(pkg, cuda, dtype, C):
 ])
 def test_bucket_sort_edges(pkg, cuda, name, sizes):
     """Ranks of 11..20 bits: one global pass by the high digit (half the
-    bits rounded up; 9 of 16), then the low bits are sorted per group (one
-    block per group of up to 512 cells; groups of 1024 cells are cut into
-    slices of 8192 keys) and the group's cell ranges written.  Cases: the smallest groups, the largest rank space,
-    one group far larger than the rest (90% of the points in 3 cells, sizes
-    not multiples of 64) with empty groups around it, and groups of exactly
-    1, 2 and 4 slices and one key more."""
+    bits rounded up; 9 of 16), then the low bits are sorted per group (groups
+    of up to 512 cells by one block, or by two blocks each taking half the
+    keys above 8192 keys; groups of 1024 cells are cut into slices of 8192
+    keys) and the group's cell ranges written.  Cases: the smallest groups,
+    the largest rank space, one group far larger than the rest (90% of the
+    points in 3 cells, sizes not multiples of 64) with empty groups around
+    it, groups of 8192, 8193 and 20,000 keys spread over the point order (one
+    block; two parts; two parts too large for registers), and groups of
+    exactly 1, 2 and 4 slices and one key more."""
     N = 120000
     feats, coords = rand_case(N, 8, *sizes, seed=11)
+    if 'part threshold' in name:
+        # rank x * 360 + y: group g (rank >> 8) holds ranks [256 g, 256 g + 256);
+        # groups 10, 20, 30 get 8192, 8193 and 20,000 points at random places
+        # of the point order, on random cells of the group
+        g = torch.Generator().manual_seed(14)
+        order = torch.randperm(N, generator=g)
+        at = 0
+        for grp, n in ((10, 8192), (20, 8193), (30, 20000)):
+            idx = order[at:at + n]
+            r = grp * 256 + torch.randint(0, 256, (n,), generator=g)
+            coords[idx, 0] = (r // 360).to(coords.dtype)
+            coords[idx, 1] = (r % 360).to(coords.dtype)
+            at += n
+        rest = order[at:]
+        r = torch.randint(0, 360 * 360, (len(rest),), generator=g)
+        r = torch.where((r >> 8 == 10) | (r >> 8 == 20) | (r >> 8 == 30), r + 256, r)
+        coords[rest, 0] = (r // 360).to(coords.dtype)
+        coords[rest, 1] = (r % 360).to(coords.dtype)
     if 'one group' in name:
         g = torch.Generator().manual_seed(12)
         hot = torch.rand(N, generator=g) < 0.9
