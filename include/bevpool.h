@@ -144,9 +144,10 @@ int bevpool_coord_ranks(const void *coords, int32_t coord_bytes, int64_t n_point
 /*
  * Stream compaction of kept points + stable radix sort of their ranks
  * + dense per-cell point ranges.  Ranks of 11..20 bits take one global pass
- * by the high digit and one block per group of equal high digit for the
- * low digit (that block also writes the group's cell ranges); other rank
- * widths take LSD passes of at most 10 bits.  Both give the same keys.  The
+ * by the high digit and, for the low digit, one block per group of equal
+ * high digit (two above 8192 keys; 8192-key slices for groups of 1024
+ * cells), which also write the group's cell ranges; other rank widths take
+ * LSD passes of at most 10 bits.  All give the same keys.  The
  * index stage's histograms must come from the quantise / coord-ranks call
  * made with the same n_cells.
  *
