@@ -7,8 +7,6 @@ workspace larger than the array, and, after a warm-up call, no change in free
 device memory and no timing records."""
 from __future__ import annotations
 
-import ctypes
-
 import pytest
 import torch
 
