@@ -151,14 +151,14 @@ def test_no_cpu_fallback(pkg):
 
 
 def test_binding_keeps_cpu_branch(pkg):
-    """The op-level binding of INTEGRATION.md replaces only the GPU branch of
-    ``bev_pool_triton.py:219-227``: CPU tensors still reach the reference's
+    """The op-level binding a maintainer adds to the reference replaces only the
+    GPU branch of ``bev_pool_triton.py:219-227``: CPU tensors still reach the reference's
     CPU fallback (restated in oracle/ for this test) and give the reference's
     known answer (``tests/test_ops/test_bev_pool.py:57-84``); calling this
     package directly with CPU tensors raises the documented error."""
     from oracle import torch_fallback as ref
 
-    def bev_pool(feats, coords, B, D, H, W):  # the binding, as INTEGRATION.md writes it
+    def bev_pool(feats, coords, B, D, H, W):  # the binding: GPU tensors to this package
         ref.check_inputs(feats, coords, B, D, H, W)
         if feats.is_cuda:
             return pkg.bev_pool(feats, coords, B, D, H, W)
