@@ -112,7 +112,8 @@ KERNEL_TIMER_NAMES = (
     ('coord_ranks_kernel', 'coord_ranks'), ('radix_scatter_kernel', 'radix_scatter'),
     ('radix_hist_kernel', 'radix_hist'), ('radix_scan_kernel', 'radix_scan'),
     ('cell_ranges_kernel', 'cell_ranges'), ('bucket_sort_kernel', 'bucket_sort'),
-    ('init_meta', 'init_meta'),
+    ('bucket_count_kernel', 'bucket_count'), ('bucket_scan_kernel', 'bucket_scan'),
+    ('bucket_place_kernel', 'bucket_place'), ('init_meta', 'init_meta'),
 )
 CALIBRATOR_BYTES = 512 << 20  # the --mode kernels copy and read-only sum
 
@@ -202,7 +203,9 @@ def main():
     # untimed steps right before the timed ones (the GPU has already run the
     # first-steps profile and the secondary figures by then)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--config', default='det', choices=sorted(WORKLOAD))
+    # the headline modes take the vtransform-level workloads; --mode kernels
+    # also the op-level bf16 configuration of the benchmark table
+    ap.add_argument('--config', default='det', choices=sorted(set(WORKLOAD) | set(CONFIG_TABLE)))
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--profile-steps', type=int, default=10,
                     help='steps run with per-kernel HIP-event timing')
@@ -226,6 +229,11 @@ def main():
               'shards by batch with no collective; run one process per GPU.', file=sys.stderr)
         sys.exit(2)
 
+    if args.config not in WORKLOAD and args.mode not in ('kernels', 'configs'):
+        print(f'--config {args.config} is an op-level configuration: only --mode kernels runs it '
+              '(--mode configs runs every configuration)', file=sys.stderr)
+        sys.exit(2)
+
     pkg = __graft_entry__.load_package()
     from bevfusion_triton_amd import _lib
 
@@ -234,6 +242,10 @@ def main():
     if args.mode == 'configs':
         for name in CONFIG_TABLE:
             print(json.dumps(config_figure(pkg, _lib, name, dev)), flush=True)
+        return
+    if args.config not in WORKLOAD:  # op level, --mode kernels (checked above)
+        case = config_case(pkg, args.config, dev, stats=False)
+        kernels_mode(lambda: case['bwd'](case['fwd']()), args, dev)
         return
     if args.mode == 'ceiling':
         print(json.dumps(access_ceiling(pkg, _lib, args.config, dev)), flush=True)
@@ -265,20 +277,7 @@ def main():
         return out, gx
 
     if args.mode == 'kernels':
-        log(f'[bench] warmup {args.warmup}')
-        for _ in range(args.warmup):
-            step()
-        for _ in range(args.steps):
-            step()
-        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        src.fill_(1)
-        for _ in range(3):
-            dst.copy_(src)  # plain copy: 512 MiB read + 512 MiB written per launch
-        for _ in range(3):
-            src.view(torch.float32).sum()  # read-only calibrator: 512 MiB read per launch
-        torch.cuda.synchronize()
-        log('[bench] kernels mode done')
+        kernels_mode(step, args, dev)
         return
 
     # The first ~30 steps of a process run up to 6% slower than later ones:
@@ -490,24 +489,43 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def config_figure(pkg, lib, name, dev):
-    """One benchmark configuration after 40 untimed steps: the time of 20
-    back-to-back fwd+bwd steps (HIP events around the loop only; `step_us`,
-    the figure the path bandwidth uses), the median fwd and bwd halves of 20
-    more steps with events between the halves, and the per-kernel averages of
-    5 more steps with the library's launch events on.
+def kernels_mode(step, args, dev):
+    """--mode kernels: warm-up and plain fwd+bwd steps, then the 512 MiB
+    traffic calibrators (a device copy and a read-only sum), for rocprofv3
+    counter passes; prints nothing on stdout."""
+    log(f'[bench] warmup {args.warmup}')
+    for _ in range(args.warmup):
+        step()
+    for _ in range(args.steps):
+        step()
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(3):
+        dst.copy_(src)  # plain copy: 512 MiB read + 512 MiB written per launch
+    for _ in range(3):
+        src.view(torch.float32).sum()  # read-only calibrator: 512 MiB read per launch
+    torch.cuda.synchronize()
+    log('[bench] kernels mode done')
+
+
+def config_case(pkg, name, dev, stats=True):
+    """The fwd and bwd calls of one benchmark configuration and its sizes.
     fp32 configurations run the vtransform-level call on the full frustum;
     bf16 runs the op-level bev_pool on the kept points (fp32 accumulation,
-    bf16 output and gradient)."""
-    log(f'[bench] config {name}')
+    bf16 output and gradient).  stats=False skips the index export that
+    counts the kept points and occupied cells (the byte counts are then
+    None), so that nothing but the configuration's own calls runs."""
     spec, geom_cpu, x = make_inputs(pkg, name, dev)
     geom = geom_cpu.to(dev)
     module = pkg.BevPoolTransform(spec.xbound, spec.ybound, spec.zbound).to(dev)
     C = spec.channels
     n_all = geom[..., 0].numel()
-    exp = pkg.LSSIndexExport(geom, module.dx, module.bx, module.nx)
-    n_kept, n_occ = int(exp.perm.numel()), int(exp.starts.numel())
-    del exp
+    n_kept = n_occ = None
+    if stats:
+        exp = pkg.LSSIndexExport(geom, module.dx, module.bx, module.nx)
+        n_kept, n_occ = int(exp.perm.numel()), int(exp.starts.numel())
+        del exp
     X, Y, Z = (int(v) for v in module.nx)
     B = spec.batch
     cells = B * X * Y * Z
@@ -523,7 +541,7 @@ def config_figure(pkg, lib, name, dev):
         def bwd(out):
             torch.autograd.grad(out, x, g)
 
-        fwd_b, bwd_b = alg_bytes(n_all, n_kept, n_occ, cells, C, s)
+        fwd_b, bwd_b = alg_bytes(n_all, n_kept, n_occ, cells, C, s) if stats else (None, None)
         level, n_step = 'vtransform', n_all
     else:
         off, d, nx = module.grid()
@@ -545,9 +563,26 @@ def config_figure(pkg, lib, name, dev):
 
         # op level: kept rows read, dense grid written; grid rows of occupied
         # cells read, kept-row gradient written (no geometry, no zero rows)
-        fwd_b = s * C * n_kept + s * C * cells
-        bwd_b = s * C * n_occ + s * C * n_kept
+        fwd_b = s * C * n_kept + s * C * cells if stats else None
+        bwd_b = s * C * n_occ + s * C * n_kept if stats else None
         level, n_step = 'op', n_kept
+    return dict(spec=spec, fwd=fwd, bwd=bwd, fwd_b=fwd_b, bwd_b=bwd_b, level=level,
+                n_step=n_step, n_all=n_all, n_kept=n_kept, n_occ=n_occ, cells=cells, B=B,
+                X=X, Y=Y, Z=Z, C=C, s=s)
+
+
+def config_figure(pkg, lib, name, dev):
+    """One benchmark configuration (``config_case``) after 40 untimed steps:
+    the time of 20 back-to-back fwd+bwd steps (HIP events around the loop
+    only; `step_us`, the figure the path bandwidth uses), the median fwd and
+    bwd halves of 20 more steps with events between the halves, and the
+    per-kernel averages of 5 more steps with the library's launch events on."""
+    log(f'[bench] config {name}')
+    case = config_case(pkg, name, dev)
+    fwd, bwd, spec = case['fwd'], case['bwd'], case['spec']
+    fwd_b, bwd_b, level, n_step = case['fwd_b'], case['bwd_b'], case['level'], case['n_step']
+    n_all, n_kept, n_occ, cells = case['n_all'], case['n_kept'], case['n_occ'], case['cells']
+    B, X, Y, Z, C, s = (case[k] for k in ('B', 'X', 'Y', 'Z', 'C', 's'))
     for _ in range(40):  # past the first steps' transient (~10 ms of this load)
         bwd(fwd())
     torch.cuda.synchronize()
