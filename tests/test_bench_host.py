@@ -101,3 +101,17 @@ def test_cpu_threads_follow_the_environment(monkeypatch):
     monkeypatch.delenv('OMP_NUM_THREADS')
     n, aff, src = bench.cpu_threads()
     assert src == 'affinity' and n == aff
+
+
+@pytest.mark.parametrize('mode', ['bench', 'ceiling'])
+def test_op_level_config_only_in_kernels_mode(monkeypatch, capsys, mode):
+    """The op-level bf16 configuration runs under --mode kernels (counter
+    passes) and --mode configs only; the headline modes refuse it before the
+    package or the GPU is touched."""
+    monkeypatch.setattr('sys.argv', ['bench.py', '--mode', mode, '--config', 'bf16'])
+    monkeypatch.setattr(bench.__graft_entry__, 'load_package',
+                        lambda: pytest.fail('the package was loaded'))
+    with pytest.raises(SystemExit) as e:
+        bench.main()
+    assert e.value.code == 2
+    assert 'op-level configuration' in capsys.readouterr().err
